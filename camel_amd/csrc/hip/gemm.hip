@@ -1,0 +1,577 @@
+// fp32 GEMM and implicit-GEMM conv2d on gfx950 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// Replaces the ijk double loop of __tensor_matmul__
+// (modules/tensor/operators.cpp:757-766) and defines conv2d / dense on the
+// same core.
+//
+// Kernel structure (one template, three operand loaders):
+//   * workgroup tile BM x BN, K consumed in stages of BK; 4 waves in a
+//     WM x WN grid, each wave owns (BM/WM) x (BN/WN) = FM x FN blocks of 32x32;
+//   * LDS holds both operands "k-quad major": plane q holds, for every row of
+//     the tile, the 4 consecutive k values 4q..4q+3 as one 16-byte chunk, so a
+//     lane fetches its 4 k values of a 32x32 block with one ds_read_b128;
+//     planes are padded by 16 bytes to spread the stores over the banks;
+//   * a 32x32x2 MFMA takes, per lane l, k = 8s + 4*(l/32) + t (t = 0..3) from
+//     that chunk: the lower half-wave covers k 0..3 of an 8-group, the upper
+//     half k 4..7, and A and B use the same mapping, so every k is summed once;
+//   * stages are double-buffered in LDS with the next stage held in registers
+//     while the current one is multiplied (one barrier per stage);
+//   * blockIdx is remapped so each of the 8 XCDs (own L2) works on a compact
+//     group of tiles, grouped GROUP_M tile-rows deep;
+//   * split-K (blockIdx.y) writes fp32 partials that a second kernel sums in
+//     split order and passes through the epilogue;
+//   * epilogue: bias (per column for dense, per row = output channel for
+//     conv) then relu as x * (x > 0), stored straight from the accumulators.
+#include "common.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace camel_hip {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int GROUP_M = 4;
+
+// Operand loader kinds.
+enum { LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2 };
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_> struct Tile {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr int THREADS = 64 * WM * WN;
+    static constexpr int WTM = BM / WM, WTN = BN / WN;
+    static constexpr int FM = WTM / 32, FN = WTN / 32;
+    static constexpr int KQ = BK / 4;
+    static constexpr int A_PLANE = BM * 4 + 4;
+    static constexpr int B_PLANE = BN * 4 + 4;
+    static constexpr int A_STAGE = KQ * A_PLANE;
+    static constexpr int B_STAGE = KQ * B_PLANE;
+    static constexpr int STAGE = A_STAGE + B_STAGE;
+    static constexpr int A_ITEMS = BM * KQ / THREADS;
+    static constexpr int B_ITEMS = KQ * (BN / 4) / THREADS;
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+    static_assert(BK % 8 == 0, "BK must be a multiple of 8");
+    static_assert((BM * KQ) % THREADS == 0, "A stage must split evenly over threads");
+    static_assert((KQ * (BN / 4)) % THREADS == 0, "B stage must split evenly over threads");
+    static_assert(THREADS % (BN / 4) == 0 || (BN / 4) % THREADS == 0, "B column mapping");
+};
+
+struct GemmArgs {
+    const float *A;  // [M, lda] row-major (conv: weights [Co, C*KH*KW])
+    const float *B;  // [K, ldb] row-major (conv: input x, NCHW)
+    float *C;        // [M, ldc] row-major (conv: output y, NCHW)
+    const float *bias;
+    float *partial;  // split-K partials [splits][M][N], or null
+    const int2 *ktab; // conv: per k {offset of (c,kh,kw) in x, kh << 16 | kw}
+    int M, N, K;
+    int lda, ldb, ldc;
+    int k_per_split;  // multiple of BK
+    int flags;
+    // conv geometry (N = batch * P columns)
+    int P, OW, H, W, CHW, stride, pad;
+};
+
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    // Workgroups are dispatched round-robin over the 8 XCDs: give XCD x the
+    // contiguous id range [x*nb/8, (x+1)*nb/8) so its L2 sees a compact block.
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int per_group = GROUP_M * tiles_n;
+    const int g = bid / per_group;
+    const int first_m = g * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int in_group = bid - g * per_group;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
+template <class T, int AMODE, int BMODE>
+__global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) float smem[2 * T::STAGE];
+
+    const int tid = threadIdx.x;
+    const int tiles_m = (g.M + T::BM - 1) / T::BM;
+    const int tiles_n = (g.N + T::BN - 1) / T::BN;
+    int tm, tn;
+    tile_coords(tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * T::BM, n0 = tn * T::BN;
+    const int kbeg = blockIdx.y * g.k_per_split;
+    const int kend = min(g.K, kbeg + g.k_per_split);
+    const int nk = kend > kbeg ? (kend - kbeg + T::BK - 1) / T::BK : 0;
+
+    float4 ra[T::A_ITEMS];
+    float4 rb[T::B_ITEMS][4];
+
+    // ---- conv: per-thread column geometry, fixed for the whole K loop ----
+    // Column c of the thread's 4 columns is n0 + nq + c*(BN/4) (spread so a
+    // wave's scalar loads touch consecutive pixels).
+    int col_base[4], col_ih[4], col_iw[4];
+    if constexpr (BMODE == LOAD_CONV) {
+        static_assert(T::THREADS % (T::BN / 4) == 0, "conv columns must be fixed per thread");
+        const int nq = tid % (T::BN / 4);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int pg = n0 + nq + c * (T::BN / 4);
+            if (pg < g.N) {
+                const int img = pg / g.P, p = pg - img * g.P;
+                const int oh = p / g.OW, ow = p - oh * g.OW;
+                col_ih[c] = oh * g.stride - g.pad;
+                col_iw[c] = ow * g.stride - g.pad;
+                col_base[c] = img * g.CHW + col_ih[c] * g.W + col_iw[c];
+            } else {
+                col_ih[c] = -(1 << 28); // never in range
+                col_iw[c] = 0;
+                col_base[c] = 0;
+            }
+        }
+    }
+
+    auto load_stage = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < T::A_ITEMS; ++i) {
+            const int q = tid + i * T::THREADS;
+            const int kq = q % T::KQ, m = q / T::KQ;
+            const int gm = m0 + m, gk = k0 + 4 * kq;
+            const float *src = g.A + (size_t)gm * g.lda + gk;
+            if constexpr (AMODE == LOAD_VEC) {
+                ra[i] = (gm < g.M && gk < kend) ? *reinterpret_cast<const float4 *>(src)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                const bool rv = gm < g.M;
+                ra[i].x = (rv && gk + 0 < kend) ? src[0] : 0.f;
+                ra[i].y = (rv && gk + 1 < kend) ? src[1] : 0.f;
+                ra[i].z = (rv && gk + 2 < kend) ? src[2] : 0.f;
+                ra[i].w = (rv && gk + 3 < kend) ? src[3] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < T::B_ITEMS; ++i) {
+            const int q = tid + i * T::THREADS;
+            const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
+            if constexpr (BMODE == LOAD_VEC) {
+                const int gn = n0 + 4 * nq;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int gk = k0 + 4 * kq + u;
+                    rb[i][u] = (gn < g.N && gk < kend)
+                                   ? *reinterpret_cast<const float4 *>(g.B + (size_t)gk * g.ldb + gn)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            } else if constexpr (BMODE == LOAD_SCALAR) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int gk = k0 + 4 * kq + u;
+                    const float *row = g.B + (size_t)gk * g.ldb;
+                    float v[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int gn = n0 + nq + c * (T::BN / 4);
+                        v[c] = (gn < g.N && gk < kend) ? row[gn] : 0.f;
+                    }
+                    rb[i][u] = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int gk = k0 + 4 * kq + u;
+                    float v[4] = {0.f, 0.f, 0.f, 0.f};
+                    if (gk < kend) {
+                        const int2 e = g.ktab[gk];
+                        const int kh = e.y >> 16, kw = e.y & 0xffff;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const int ih = col_ih[c] + kh, iw = col_iw[c] + kw;
+                            if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+                                v[c] = g.B[(size_t)(col_base[c] + e.x)];
+                        }
+                    }
+                    rb[i][u] = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
+        }
+    };
+
+    auto store_stage = [&](float *As, float *Bs) {
+#pragma unroll
+        for (int i = 0; i < T::A_ITEMS; ++i) {
+            const int q = tid + i * T::THREADS;
+            const int kq = q % T::KQ, m = q / T::KQ;
+            *reinterpret_cast<float4 *>(As + kq * T::A_PLANE + m * 4) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < T::B_ITEMS; ++i) {
+            const int q = tid + i * T::THREADS;
+            const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
+            float *plane = Bs + kq * T::B_PLANE;
+            // rb[i][u] holds row k0+4kq+u for 4 columns; LDS wants, per column,
+            // the 4 k values as one chunk: a 4x4 transpose in registers.
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int n = (BMODE == LOAD_VEC) ? 4 * nq + c : nq + c * (T::BN / 4);
+                float4 col;
+                col.x = rb[i][0][c];
+                col.y = rb[i][1][c];
+                col.z = rb[i][2][c];
+                col.w = rb[i][3][c];
+                *reinterpret_cast<float4 *>(plane + n * 4) = col;
+            }
+        }
+    };
+
+    const int wave = tid >> 6, lane = tid & 63;
+    const int half = lane >> 5, r32 = lane & 31;
+    const int wm = wave / T::WN, wn = wave % T::WN;
+
+    floatx16 acc[T::FM][T::FN];
+#pragma unroll
+    for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    if (nk > 0) {
+        load_stage(kbeg);
+        store_stage(smem, smem + T::A_STAGE);
+        __syncthreads();
+    }
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const bool more = kt + 1 < nk;
+        if (more) load_stage(kbeg + (kt + 1) * T::BK);
+        const float *As = smem + (kt & 1) * T::STAGE;
+        const float *Bs = As + T::A_STAGE;
+        const float *a_base = As + half * T::A_PLANE + (wm * T::WTM + r32) * 4;
+        const float *b_base = Bs + half * T::B_PLANE + (wn * T::WTN + r32) * 4;
+#pragma unroll
+        for (int s8 = 0; s8 < T::BK / 8; ++s8) {
+            float4 a[T::FM], b[T::FN];
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+                a[i] = *reinterpret_cast<const float4 *>(a_base + 2 * s8 * T::A_PLANE + i * 128);
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j)
+                b[j] = *reinterpret_cast<const float4 *>(b_base + 2 * s8 * T::B_PLANE + j * 128);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < T::FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t],
+                                                                          acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            float *nxt = smem + ((kt + 1) & 1) * T::STAGE;
+            store_stage(nxt, nxt + T::A_STAGE);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue ----
+    const bool has_bias = (g.flags & CAMEL_EPI_BIAS) != 0 && g.partial == nullptr;
+    const bool has_relu = (g.flags & CAMEL_EPI_RELU) != 0 && g.partial == nullptr;
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) {
+        const int col = n0 + wn * T::WTN + j * 32 + r32;
+        if (col >= g.N) continue;
+        size_t col_off = col;
+        if constexpr (BMODE == LOAD_CONV) {
+            const int img = col / g.P, p = col - img * g.P;
+            col_off = (size_t)img * g.M * g.P + p;
+        }
+        const float bias_col = (has_bias && BMODE != LOAD_CONV) ? g.bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * T::WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                if (row >= g.M) continue;
+                float x = acc[i][j][v];
+                if (g.partial) {
+                    g.partial[(size_t)blockIdx.y * g.M * g.N + (size_t)row * g.N + col] = x;
+                    continue;
+                }
+                if (has_bias) x = x + (BMODE == LOAD_CONV ? g.bias[row] : bias_col);
+                if (has_relu) x = relu_idiom(x);
+                if constexpr (BMODE == LOAD_CONV)
+                    g.C[col_off + (size_t)row * g.P] = x;
+                else
+                    g.C[(size_t)row * g.ldc + col] = x;
+            }
+        }
+    }
+}
+
+// Sums split-K partials in split order, then bias and relu.
+__global__ void splitk_reduce_kernel(const float *partial, int splits, float *C, int M, int N,
+                                     int ldc, const float *bias, int flags) {
+    const size_t total = (size_t)M * N;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        float s = partial[idx];
+        for (int z = 1; z < splits; ++z) s = s + partial[(size_t)z * total + idx];
+        const int row = (int)(idx / N), col = (int)(idx % N);
+        if (flags & CAMEL_EPI_BIAS) s = s + bias[col];
+        if (flags & CAMEL_EPI_RELU) s = relu_idiom(s);
+        C[(size_t)row * ldc + col] = s;
+    }
+}
+
+// Mixed-dtype matmul: one thread per output, double accumulation in k order
+// exactly as operators.cpp:757-766, rounded through setFromDouble.
+__global__ void matmul_generic_kernel(int adt, const void *A, int bdt, const void *B, int odt,
+                                      void *C, int M, int N, int K) {
+    const int64_t total = (int64_t)M * N;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int64_t i = idx / N, j = idx % N;
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; ++k)
+            acc += load_as_double(adt, A, i * K + k) * load_as_double(bdt, B, k * N + j);
+        store_from_double(odt, C, idx, acc);
+    }
+}
+
+// ---- host-side launch -----------------------------------------------------------
+
+using TileBig = Tile<256, 256, 16, 2, 2>;   // wave 128x128
+using TileMid = Tile<128, 128, 32, 2, 2>;   // wave 64x64
+using TileSmall = Tile<64, 64, 64, 2, 2>;   // wave 32x32
+using TileSkinny = Tile<32, 256, 32, 1, 4>; // wave 32x64
+using TileConv = Tile<128, 256, 16, 2, 2>;  // wave 64x128
+using TileConv64 = Tile<64, 256, 32, 1, 4>; // wave 64x64
+
+template <class T> int64_t tiles_of(int64_t M, int64_t N) {
+    return ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
+}
+
+template <class T, int AMODE, int BMODE> int launch(GemmArgs g, int splits, const char *name) {
+    const int64_t tiles = tiles_of<T>(g.M, g.N);
+    dim3 grid((unsigned)tiles, (unsigned)splits);
+    hipLaunchKernelGGL((sgemm_kernel<T, AMODE, BMODE>), grid, dim3(T::THREADS), 0, stream(), g);
+    return check_launch(name);
+}
+
+template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool bvec) {
+    if (avec && bvec) return launch<T, LOAD_VEC, LOAD_VEC>(g, splits, "sgemm_kernel");
+    if (avec) return launch<T, LOAD_VEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
+    if (bvec) return launch<T, LOAD_SCALAR, LOAD_VEC>(g, splits, "sgemm_kernel");
+    return launch<T, LOAD_SCALAR, LOAD_SCALAR>(g, splits, "sgemm_kernel");
+}
+
+// Scratch for split-K partials, grown on demand (kept for the process).
+float *g_partial = nullptr;
+size_t g_partial_bytes = 0;
+
+int ensure_partial(size_t bytes) {
+    if (bytes <= g_partial_bytes) return CAMEL_HIP_OK;
+    if (g_partial) {
+        CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+        camel_hip_free(g_partial);
+        g_partial = nullptr;
+        g_partial_bytes = 0;
+    }
+    void *p = nullptr;
+    CAMEL_RETURN_IF(camel_hip_malloc(&p, bytes));
+    g_partial = static_cast<float *>(p);
+    g_partial_bytes = bytes;
+    return CAMEL_HIP_OK;
+}
+
+enum class Cfg { Big, Mid, Small, Skinny };
+
+// Picks a tile shape and split count so the grid covers the chip's CUs.
+void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int &bk) {
+    splits = 1;
+    int64_t tiles;
+    if (M <= 32) {
+        cfg = Cfg::Skinny;
+        bk = TileSkinny::BK;
+        tiles = tiles_of<TileSkinny>(M, N);
+    } else if (tiles_of<TileBig>(M, N) >= cus) {
+        cfg = Cfg::Big;
+        bk = TileBig::BK;
+        return;
+    } else if (tiles_of<TileMid>(M, N) >= cus) {
+        cfg = Cfg::Mid;
+        bk = TileMid::BK;
+        return;
+    } else {
+        cfg = Cfg::Small;
+        bk = TileSmall::BK;
+        tiles = tiles_of<TileSmall>(M, N);
+        if (tiles >= cus) return;
+    }
+    // Split K so tiles*splits fills the chip, keeping >= 4 stages per split.
+    const int64_t want = (cus + tiles - 1) / tiles;
+    const int64_t max_splits = std::max<int64_t>(1, K / (4 * bk));
+    splits = (int)std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(max_splits, 64)));
+}
+
+} // namespace
+} // namespace camel_hip
+
+using namespace camel_hip;
+
+extern "C" {
+
+int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
+                    const float *bias, int flags) {
+    if (M < 0 || N < 0 || K < 0) return fail(CAMEL_HIP_ERR_SHAPE, "sgemm: negative dimension");
+    if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
+        return fail(CAMEL_HIP_ERR_SHAPE, "sgemm: dimension too large");
+    if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, "sgemm: null bias");
+    if (M == 0 || N == 0) return ok();
+    if (!C || (K > 0 && (!A || !B))) return fail(CAMEL_HIP_ERR_ARG, "sgemm: null operand");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    GemmArgs g{};
+    g.A = A;
+    g.B = B;
+    g.C = C;
+    g.bias = bias;
+    g.M = (int)M;
+    g.N = (int)N;
+    g.K = (int)K;
+    g.lda = (int)K;
+    g.ldb = (int)N;
+    g.ldc = (int)N;
+    g.flags = flags;
+    const bool avec = (K % 4 == 0) && ((uintptr_t)A % 16 == 0);
+    const bool bvec = (N % 4 == 0) && ((uintptr_t)B % 16 == 0);
+    Cfg cfg;
+    int splits, bk;
+    choose(M, N, K, device_cu_count(), cfg, splits, bk);
+    int64_t kps = (K + splits - 1) / splits;
+    kps = (kps + bk - 1) / bk * bk;
+    if (kps == 0) kps = bk;
+    splits = (int)std::max<int64_t>(1, (K + kps - 1) / kps);
+    g.k_per_split = (int)kps;
+    if (splits > 1) {
+        CAMEL_RETURN_IF(ensure_partial((size_t)splits * M * N * sizeof(float)));
+        g.partial = g_partial;
+    }
+    int rc;
+    switch (cfg) {
+    case Cfg::Big:
+        rc = launch_gemm_modes<TileBig>(g, splits, avec, bvec);
+        break;
+    case Cfg::Mid:
+        rc = launch_gemm_modes<TileMid>(g, splits, avec, bvec);
+        break;
+    case Cfg::Small:
+        rc = launch_gemm_modes<TileSmall>(g, splits, avec, bvec);
+        break;
+    default:
+        rc = launch_gemm_modes<TileSkinny>(g, splits, avec, bvec);
+        break;
+    }
+    CAMEL_RETURN_IF(rc);
+    if (splits > 1) {
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(M * N, 256)), dim3(256), 0,
+                           stream(), g_partial, splits, C, (int)M, (int)N, (int)N, bias, flags);
+        CAMEL_RETURN_IF(check_launch("splitk_reduce_kernel"));
+    }
+    return ok();
+}
+
+int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int odt, void *C,
+                             int64_t M, int64_t N, int64_t K) {
+    if (!valid_dtype(adt) || !valid_dtype(bdt) || !valid_dtype(odt))
+        return fail(CAMEL_HIP_ERR_DTYPE, "matmul: unsupported dtype");
+    if (M < 0 || N < 0 || K < 0) return fail(CAMEL_HIP_ERR_SHAPE, "matmul: negative dimension");
+    if (M == 0 || N == 0) return ok();
+    if (!C || (K > 0 && (!A || !B))) return fail(CAMEL_HIP_ERR_ARG, "matmul: null operand");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    hipLaunchKernelGGL(matmul_generic_kernel, dim3(grid_for(M * N, 256)), dim3(256), 0, stream(),
+                       adt, A, bdt, B, odt, C, (int)M, (int)N, (int)K);
+    CAMEL_RETURN_IF(check_launch("matmul_generic_kernel"));
+    return ok();
+}
+
+int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y, int64_t N,
+                     int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
+                     int64_t stride, int64_t pad, int flags) {
+    if (N < 0 || C <= 0 || H <= 0 || W <= 0 || Co <= 0 || KH <= 0 || KW <= 0 || stride <= 0 ||
+        pad < 0)
+        return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: invalid geometry");
+    if (H + 2 * pad < KH || W + 2 * pad < KW)
+        return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: kernel larger than padded input");
+    if (KH > 0xffff || KW > 0xffff) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: kernel too large");
+    const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    const int64_t K = C * KH * KW, P = OH * OW, NP = N * P;
+    if (N * C * H * W > INT32_MAX || NP > INT32_MAX || N * Co * P > INT32_MAX || Co * K > INT32_MAX)
+        return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: tensor too large");
+    if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, "conv2d: null bias");
+    if (N == 0) return ok();
+    if (!x || !w || !y) return fail(CAMEL_HIP_ERR_ARG, "conv2d: null operand");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    // k -> (c, kh, kw) table, built on the host once per geometry.
+    static std::vector<int2> host_tab;
+    static int2 *dev_tab = nullptr;
+    static int64_t tab_cap = 0;
+    static int64_t tab_key[4] = {-1, -1, -1, -1};
+    if (tab_key[0] != C || tab_key[1] != KH || tab_key[2] != KW || tab_key[3] != H * W * 65536 + W) {
+        if (K > tab_cap) {
+            if (dev_tab) {
+                CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+                camel_hip_free(dev_tab);
+            }
+            void *p = nullptr;
+            CAMEL_RETURN_IF(camel_hip_malloc(&p, (size_t)K * sizeof(int2)));
+            dev_tab = static_cast<int2 *>(p);
+            tab_cap = K;
+        }
+        host_tab.resize((size_t)K);
+        for (int64_t k = 0; k < K; ++k) {
+            const int64_t c = k / (KH * KW), r = k % (KH * KW), kh = r / KW, kw = r % KW;
+            host_tab[(size_t)k] = make_int2((int)(c * H * W + kh * W + kw), (int)((kh << 16) | kw));
+        }
+        CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dev_tab, host_tab.data(), (size_t)K * sizeof(int2),
+                                                 hipMemcpyHostToDevice, stream()),
+                                  "hipMemcpyAsync(conv table)"));
+        CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+        tab_key[0] = C;
+        tab_key[1] = KH;
+        tab_key[2] = KW;
+        tab_key[3] = H * W * 65536 + W;
+    }
+    GemmArgs g{};
+    g.A = w;
+    g.B = x;
+    g.C = y;
+    g.bias = bias;
+    g.ktab = dev_tab;
+    g.M = (int)Co;
+    g.N = (int)NP;
+    g.K = (int)K;
+    g.lda = (int)K;
+    g.flags = flags;
+    g.P = (int)P;
+    g.OW = (int)OW;
+    g.H = (int)H;
+    g.W = (int)W;
+    g.CHW = (int)(C * H * W);
+    g.stride = (int)stride;
+    g.pad = (int)pad;
+    const bool avec = (K % 4 == 0) && ((uintptr_t)w % 16 == 0);
+    int rc;
+    if (Co <= 64) {
+        g.k_per_split = (int)((K + TileConv64::BK - 1) / TileConv64::BK * TileConv64::BK);
+        rc = avec ? launch<TileConv64, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
+                  : launch<TileConv64, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
+    } else {
+        g.k_per_split = (int)((K + TileConv::BK - 1) / TileConv::BK * TileConv::BK);
+        rc = avec ? launch<TileConv, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
+                  : launch<TileConv, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
+    }
+    CAMEL_RETURN_IF(rc);
+    return ok();
+}
+
+} // extern "C"

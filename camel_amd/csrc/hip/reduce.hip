@@ -1,0 +1,399 @@
+// Row softmax and the rank-2 reductions (sum / max / argmax along an axis,
+// whole-tensor sum).
+//
+// Softmax fuses the nine-operator composition of test/run/nn/mnist.cml:13-25
+// into one pass, op for op:
+//   m  = first strict-'>' row max (tensorMaxAxis, runtime.cpp:924-963)
+//   mb = fl32(0.0 + m*1.0)         (reshape(m) @ ones([1,k]) broadcast)
+//   e  = fl32(exp(double(fl32(x - mb))))   (subtract, tensorExp 1013-1026)
+//   s  = fl32(sum_j double(e_j))   (tensorSumAxis 887-922, fp64 accumulation)
+//   y  = fl32(e / s)               (divide, "Division by zero" if s == 0)
+// One wave owns one row; rows up to 64*4*ITEMS columns stay in registers, so
+// HBM sees one read and one write per element (8 B/elem).  The fp64 sum
+// differs from the reference's sequential order only in the last bits of
+// the double, below the fp32 rounding of s.
+//
+// Max/argmax reductions across lanes keep (value, index) pairs and prefer the
+// lower index on ties, which reproduces "first element, then strict '>'",
+// including the order of +0/-0; NaN never wins except as element 0.
+#include "common.h"
+
+#include <cmath>
+
+namespace camel_hip {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+constexpr int NO_INDEX = 0x7fffffff;
+
+struct Best {
+    float v;
+    int i;
+};
+
+// b wins over a if it is a real candidate and larger, or equal and earlier.
+__device__ __forceinline__ Best best_of(Best a, Best b) {
+    if (b.i == NO_INDEX) return a;
+    if (a.i == NO_INDEX) return b;
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
+__device__ __forceinline__ Best wave_best(Best b) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        Best o;
+        o.v = __shfl_xor(b.v, off);
+        o.i = __shfl_xor(b.i, off);
+        b = best_of(b, o);
+    }
+    return b;
+}
+
+__device__ __forceinline__ double wave_sum(double s) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    return s;
+}
+
+// Candidate for a value at column index `idx`: NaN is skipped (a NaN never
+// compares greater); element 0 is handled by the caller.
+__device__ __forceinline__ Best candidate(float v, int idx) {
+    Best b;
+    b.v = v;
+    b.i = (v == v) ? idx : NO_INDEX;
+    return b;
+}
+
+// ITEMS float4 per lane (VEC) or ITEMS*4 scalars per lane (!VEC).
+template <int ITEMS, bool VEC>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restrict__ x,
+                                                           float *__restrict__ y, int64_t rows,
+                                                           int cols, int *flag) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * cols;
+    float *yr = y + row * cols;
+    constexpr int NV = ITEMS * 4;
+    float v[NV];
+    // Column of slot j (VEC: 4 consecutive columns per float4).
+    auto col_of = [&](int j) -> int {
+        return VEC ? 4 * (lane + WAVE * (j >> 2)) + (j & 3) : lane + WAVE * j;
+    };
+    if constexpr (VEC) {
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it) {
+            const int c = 4 * (lane + WAVE * it);
+            f4 t = {0.f, 0.f, 0.f, 0.f};
+            if (c < cols) t = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + c));
+            v[4 * it + 0] = t.x;
+            v[4 * it + 1] = t.y;
+            v[4 * it + 2] = t.z;
+            v[4 * it + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = col_of(j);
+            v[j] = c < cols ? xr[c] : 0.f;
+        }
+    }
+    Best b{0.f, NO_INDEX};
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (col_of(j) < cols) b = best_of(b, candidate(v[j], col_of(j)));
+    b = wave_best(b);
+    const float x0 = __shfl(v[0], 0);
+    const float m = (x0 != x0) ? x0 : b.v;
+    const float mb = m + 0.0f; // fl32(0.0 + m * 1.0): -0.0 becomes +0.0
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (col_of(j) < cols) {
+            v[j] = (float)exp((double)(v[j] - mb));
+            s += (double)v[j];
+        }
+    }
+    s = wave_sum(s);
+    const float s32 = (float)s + 0.0f;
+    if (s32 == 0.0f && lane == 0) *flag = 1;
+    if constexpr (VEC) {
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it) {
+            const int c = 4 * (lane + WAVE * it);
+            if (c < cols) {
+                f4 t;
+                t.x = v[4 * it + 0] / s32;
+                t.y = v[4 * it + 1] / s32;
+                t.z = v[4 * it + 2] / s32;
+                t.w = v[4 * it + 3] / s32;
+                __builtin_nontemporal_store(t, reinterpret_cast<f4 *>(yr + c));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = col_of(j);
+            if (c < cols) yr[c] = v[j] / s32;
+        }
+    }
+}
+
+// Rows longer than the register budget: three passes over the row.
+__global__ __launch_bounds__(256) void softmax_rows_long_kernel(const float *__restrict__ x,
+                                                                float *__restrict__ y,
+                                                                int64_t rows, int64_t cols,
+                                                                int *flag) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * cols;
+    float *yr = y + row * cols;
+    Best b{0.f, NO_INDEX};
+    for (int64_t c = lane; c < cols; c += WAVE) b = best_of(b, candidate(xr[c], (int)c));
+    b = wave_best(b);
+    const float x0 = xr[0];
+    const float mb = ((x0 != x0) ? x0 : b.v) + 0.0f;
+    double s = 0.0;
+    for (int64_t c = lane; c < cols; c += WAVE) s += (double)(float)exp((double)(xr[c] - mb));
+    s = wave_sum(s);
+    const float s32 = (float)s + 0.0f;
+    if (s32 == 0.0f && lane == 0) *flag = 1;
+    for (int64_t c = lane; c < cols; c += WAVE) yr[c] = (float)exp((double)(xr[c] - mb)) / s32;
+}
+
+// axis = 1: one wave per row.  kind 0 = sum, 1 = max, 2 = argmax.
+__global__ __launch_bounds__(256) void reduce_rows_kernel(int kind, int dt, const void *x,
+                                                          int64_t rows, int64_t cols, void *out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t base = row * cols;
+    if (kind == 0) {
+        double s = 0.0;
+        for (int64_t c = lane; c < cols; c += WAVE) s += load_as_double(dt, x, base + c);
+        s = wave_sum(s);
+        if (lane == 0) static_cast<float *>(out)[row] = (float)s;
+        return;
+    }
+    // Values compare as doubles (exact for fp32 and bool; int64 as the
+    // reference converts it).  Track them as double to keep int64 order.
+    double bv = 0.0;
+    int64_t bi = INT64_MAX;
+    for (int64_t c = lane; c < cols; c += WAVE) {
+        const double v = load_as_double(dt, x, base + c);
+        if (v != v) continue;
+        if (bi == INT64_MAX || v > bv) {
+            bv = v;
+            bi = c;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const double ov = __shfl_xor(bv, off);
+        const int64_t oi = __shfl_xor(bi, off);
+        if (oi != INT64_MAX && (bi == INT64_MAX || ov > bv || (ov == bv && oi < bi))) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        const double x0 = load_as_double(dt, x, base);
+        if (x0 != x0 || bi == INT64_MAX) {
+            bv = x0;
+            bi = 0;
+        }
+        if (kind == 1)
+            static_cast<float *>(out)[row] = (float)bv;
+        else
+            static_cast<int64_t *>(out)[row] = bi;
+    }
+}
+
+// axis = 0: one thread per column, rows in the reference's order (exact).
+__global__ void reduce_cols_kernel(int kind, int dt, const void *x, int64_t rows, int64_t cols,
+                                   void *out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < cols; j += stride) {
+        if (kind == 0) {
+            double acc = 0.0;
+            for (int64_t i = 0; i < rows; ++i) acc += load_as_double(dt, x, i * cols + j);
+            static_cast<float *>(out)[j] = (float)acc;
+        } else {
+            double best = load_as_double(dt, x, j);
+            int64_t best_i = 0;
+            for (int64_t i = 1; i < rows; ++i) {
+                const double v = load_as_double(dt, x, i * cols + j);
+                if (v > best) {
+                    best = v;
+                    best_i = i;
+                }
+            }
+            if (kind == 1)
+                static_cast<float *>(out)[j] = (float)best;
+            else
+                static_cast<int64_t *>(out)[j] = best_i;
+        }
+    }
+}
+
+// Whole-tensor sum: per-block fp64 partials, then one block folds them.
+__global__ __launch_bounds__(256) void sum_partial_kernel(int dt, const void *x, int64_t n,
+                                                          double *partial) {
+    __shared__ double lds[256 / WAVE];
+    double s = 0.0;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        s += load_as_double(dt, x, i);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < (int)(blockDim.x / WAVE); ++w) t += lds[w];
+        partial[blockIdx.x] = t;
+    }
+}
+
+__global__ __launch_bounds__(256) void sum_final_kernel(const double *partial, int count,
+                                                        double *result) {
+    __shared__ double lds[256 / WAVE];
+    double s = 0.0;
+    for (int i = threadIdx.x; i < count; i += blockDim.x) s += partial[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int w = 0; w < (int)(blockDim.x / WAVE); ++w) t += lds[w];
+        *result = t;
+    }
+}
+
+template <int ITEMS> int launch_softmax(const float *x, float *y, int64_t rows, int cols, bool vec) {
+    dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    if (vec)
+        hipLaunchKernelGGL((softmax_rows_kernel<ITEMS, true>), grid, block, 0, stream(), x, y, rows,
+                           cols, error_flag());
+    else
+        hipLaunchKernelGGL((softmax_rows_kernel<ITEMS, false>), grid, block, 0, stream(), x, y,
+                           rows, cols, error_flag());
+    return check_launch("softmax_rows_kernel");
+}
+
+int check_axis(int64_t rows, int64_t cols, int64_t &axis, const char *what) {
+    if (rows < 0 || cols < 0) return fail(CAMEL_HIP_ERR_SHAPE, std::string(what) + ": negative shape");
+    if (axis < 0) axis += 2;
+    if (axis != 0 && axis != 1)
+        return fail(CAMEL_HIP_ERR_SHAPE,
+                    std::string(what) + "(axis): axis must be 0 or 1 for rank-2 tensors");
+    return CAMEL_HIP_OK;
+}
+
+int reduce_axis(int kind, int dt, const void *x, int64_t rows, int64_t cols, int64_t axis,
+                void *out, const char *what) {
+    if (!valid_dtype(dt)) return fail(CAMEL_HIP_ERR_DTYPE, std::string(what) + ": unsupported dtype");
+    CAMEL_RETURN_IF(check_axis(rows, cols, axis, what));
+    const int64_t out_n = axis == 0 ? cols : rows;
+    const int64_t red_n = axis == 0 ? rows : cols;
+    if (out_n == 0) return ok();
+    if (red_n == 0 && kind != 0)
+        return fail(CAMEL_HIP_ERR_SHAPE, std::string(what) + ": reduction over an empty axis");
+    if (!out || (red_n > 0 && !x)) return fail(CAMEL_HIP_ERR_ARG, std::string(what) + ": null pointer");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    if (axis == 1) {
+        hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                           stream(), kind, dt, x, rows, cols, out);
+        CAMEL_RETURN_IF(check_launch("reduce_rows_kernel"));
+    } else {
+        hipLaunchKernelGGL(reduce_cols_kernel, dim3(grid_for(cols, 256, 16)), dim3(256), 0,
+                           stream(), kind, dt, x, rows, cols, out);
+        CAMEL_RETURN_IF(check_launch("reduce_cols_kernel"));
+    }
+    return ok();
+}
+
+} // namespace
+} // namespace camel_hip
+
+using namespace camel_hip;
+
+extern "C" {
+
+int camel_hip_softmax_rows(const float *x, float *y, int64_t rows, int64_t cols) {
+    if (rows < 0 || cols < 0) return fail(CAMEL_HIP_ERR_SHAPE, "softmax: negative shape");
+    if (rows == 0 || cols == 0) return ok();
+    if (!x || !y) return fail(CAMEL_HIP_ERR_ARG, "softmax: null pointer");
+    if (cols > INT32_MAX / 2) return fail(CAMEL_HIP_ERR_SHAPE, "softmax: row too long");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(clear_error_flag());
+    const bool vec = (cols % 4 == 0) && (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
+    const int c = (int)cols;
+    if (cols <= 64 * 4)
+        CAMEL_RETURN_IF(launch_softmax<1>(x, y, rows, c, vec));
+    else if (cols <= 64 * 8)
+        CAMEL_RETURN_IF(launch_softmax<2>(x, y, rows, c, vec));
+    else if (cols <= 64 * 16)
+        CAMEL_RETURN_IF(launch_softmax<4>(x, y, rows, c, vec));
+    else if (cols <= 64 * 32)
+        CAMEL_RETURN_IF(launch_softmax<8>(x, y, rows, c, vec));
+    else {
+        hipLaunchKernelGGL(softmax_rows_long_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                           stream(), x, y, rows, cols, error_flag());
+        CAMEL_RETURN_IF(check_launch("softmax_rows_long_kernel"));
+    }
+    int flag = 0;
+    CAMEL_RETURN_IF(read_error_flag(&flag));
+    if (flag) return fail(CAMEL_HIP_ERR_DIV_ZERO, "Division by zero");
+    return ok();
+}
+
+int camel_hip_sum_axis(int dt, const void *x, int64_t rows, int64_t cols, int64_t axis,
+                       float *out) {
+    return reduce_axis(0, dt, x, rows, cols, axis, out, "sum");
+}
+
+int camel_hip_max_axis(int dt, const void *x, int64_t rows, int64_t cols, int64_t axis,
+                       float *out) {
+    return reduce_axis(1, dt, x, rows, cols, axis, out, "max");
+}
+
+int camel_hip_argmax_axis(int dt, const void *x, int64_t rows, int64_t cols, int64_t axis,
+                          int64_t *out) {
+    return reduce_axis(2, dt, x, rows, cols, axis, out, "argmax");
+}
+
+int camel_hip_sum(int dt, const void *x, int64_t n, double *result) {
+    if (!valid_dtype(dt)) return fail(CAMEL_HIP_ERR_DTYPE, "sum: unsupported dtype");
+    if (!result || n < 0) return fail(CAMEL_HIP_ERR_ARG, "sum: bad argument");
+    if (n == 0) {
+        *result = 0.0;
+        return ok();
+    }
+    if (!x) return fail(CAMEL_HIP_ERR_ARG, "sum: null input");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    const unsigned blocks = grid_for(n, 256, 4);
+    void *ws = nullptr;
+    CAMEL_RETURN_IF(camel_hip_malloc(&ws, (blocks + 1) * sizeof(double)));
+    double *partial = static_cast<double *>(ws);
+    hipLaunchKernelGGL(sum_partial_kernel, dim3(blocks), dim3(256), 0, stream(), dt, x, n, partial);
+    int rc = check_launch("sum_partial_kernel");
+    if (rc == CAMEL_HIP_OK) {
+        hipLaunchKernelGGL(sum_final_kernel, dim3(1), dim3(256), 0, stream(), partial, (int)blocks,
+                           partial + blocks);
+        rc = check_launch("sum_final_kernel");
+    }
+    if (rc == CAMEL_HIP_OK)
+        rc = camel_hip_d2h(result, partial + blocks, sizeof(double));
+    camel_hip_free(ws);
+    CAMEL_RETURN_IF(rc);
+    return ok();
+}
+
+} // extern "C"

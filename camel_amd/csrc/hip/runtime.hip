@@ -1,0 +1,369 @@
+// Runtime part of libcamel_hip.so: device selection, the single stream, the
+// pooled device allocator, boundary copies, events and the creation kernels.
+#include "common.h"
+
+#include <cstring>
+#include <unordered_map>
+#include <vector>
+
+namespace camel_hip {
+
+namespace {
+
+struct State {
+    bool initialised = false;
+    int device = -1;
+    int cu_count = 256;
+    hipStream_t stream = nullptr;
+    int *flag = nullptr;
+    // Pool: exact-size free lists over rounded sizes; blocks never shrink.
+    std::unordered_map<size_t, std::vector<void *>> free_lists;
+    std::unordered_map<void *, size_t> live;
+    size_t in_use = 0;
+    size_t cached = 0;
+};
+
+State &state() {
+    static State s;
+    return s;
+}
+
+thread_local std::string t_last_error;
+
+// Rounded block size: 512 B granules below 1 MiB, 2 MiB granules above, so
+// tensors of one shape reuse one block and large tensors do not fragment.
+size_t round_size(size_t bytes) {
+    if (bytes == 0) bytes = 1;
+    if (bytes < (1u << 20)) return (bytes + 511) & ~size_t(511);
+    const size_t g = size_t(2) << 20;
+    return (bytes + g - 1) / g * g;
+}
+
+} // namespace
+
+std::recursive_mutex &lib_mutex() {
+    static std::recursive_mutex m;
+    return m;
+}
+
+int fail(int status, const std::string &message) {
+    t_last_error = message;
+    return status;
+}
+
+int ok() {
+    t_last_error.clear();
+    return CAMEL_HIP_OK;
+}
+
+int check_hip(hipError_t err, const char *what) {
+    if (err == hipSuccess) return CAMEL_HIP_OK;
+    return fail(CAMEL_HIP_ERR_RUNTIME, std::string(what) + ": " + hipGetErrorString(err));
+}
+
+int check_launch(const char *kernel) { return check_hip(hipGetLastError(), kernel); }
+
+hipStream_t stream() { return state().stream; }
+int device_cu_count() { return state().cu_count; }
+int *error_flag() { return state().flag; }
+
+namespace {
+
+__global__ void fill_i32_kernel(int *p, int n, int v) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+int init_device(int device) {
+    State &s = state();
+    if (s.initialised) {
+        if (device == s.device) return CAMEL_HIP_OK;
+        return fail(CAMEL_HIP_ERR_ARG, "camel_hip_init: already initialised on another device");
+    }
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(CAMEL_HIP_ERR_NO_DEVICE, "camel_hip_init: no HIP device visible");
+    if (device < 0 || device >= count)
+        return fail(CAMEL_HIP_ERR_ARG, "camel_hip_init: device index out of range");
+    CAMEL_RETURN_IF(check_hip(hipSetDevice(device), "hipSetDevice"));
+    hipDeviceProp_t prop;
+    CAMEL_RETURN_IF(check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties"));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(CAMEL_HIP_ERR_NO_DEVICE,
+                    std::string("camel_hip_init: built for gfx950, device is ") + prop.gcnArchName);
+    s.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    // Default priority, non-blocking with respect to the legacy null stream.
+    CAMEL_RETURN_IF(check_hip(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking),
+                              "hipStreamCreateWithFlags"));
+    CAMEL_RETURN_IF(check_hip(hipMalloc(&s.flag, 256), "hipMalloc(error flag)"));
+    s.device = device;
+    s.initialised = true;
+    return clear_error_flag();
+}
+
+} // namespace
+
+int ensure_init() {
+    CAMEL_LOCK();
+    if (state().initialised) return CAMEL_HIP_OK;
+    return init_device(0);
+}
+
+int clear_error_flag() {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, stream(), error_flag(), 1, 0);
+    return check_launch("fill_i32_kernel");
+}
+
+int read_error_flag(int *value) {
+    CAMEL_RETURN_IF(check_hip(
+        hipMemcpyAsync(value, error_flag(), sizeof(int), hipMemcpyDeviceToHost, stream()),
+        "hipMemcpyAsync(error flag)"));
+    return check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+}
+
+// ---- creation kernels -------------------------------------------------------------
+
+namespace {
+
+__global__ void fill_f32_kernel(float4 *p4, float *p, int64_t n, float v) {
+    int64_t n4 = n / 4;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t i = tid; i < n4; i += stride) p4[i] = make_float4(v, v, v, v);
+    for (int64_t i = n4 * 4 + tid; i < n; i += stride) p[i] = v;
+}
+
+__global__ void fill_generic_kernel(int dt, void *p, int64_t n, double v) {
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        store_from_double(dt, p, i, v);
+}
+
+__global__ void eye_kernel(float *p, int64_t n) {
+    int64_t total = n * n;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
+        p[i] = (i / n == i % n) ? 1.0f : 0.0f;
+}
+
+__global__ void arange_kernel(int64_t *p, int64_t start, int64_t step, int64_t count) {
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride)
+        p[i] = start + i * step;
+}
+
+} // namespace
+
+} // namespace camel_hip
+
+using namespace camel_hip;
+
+extern "C" {
+
+int camel_hip_init(int device) {
+    CAMEL_LOCK();
+    int rc = init_device(device);
+    return rc == CAMEL_HIP_OK ? ok() : rc;
+}
+
+int camel_hip_device_count(int *count) {
+    if (!count) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_device_count: null output");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return ok();
+}
+
+const char *camel_hip_last_error(void) { return t_last_error.c_str(); }
+
+int camel_hip_sync(void) {
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+    return ok();
+}
+
+void *camel_hip_stream(void) {
+    CAMEL_LOCK();
+    if (ensure_init() != CAMEL_HIP_OK) return nullptr;
+    return (void *)stream();
+}
+
+int camel_hip_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_malloc: null output");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    State &s = state();
+    size_t size = round_size(bytes);
+    auto it = s.free_lists.find(size);
+    if (it != s.free_lists.end() && !it->second.empty()) {
+        *ptr = it->second.back();
+        it->second.pop_back();
+        s.cached -= size;
+    } else {
+        void *p = nullptr;
+        hipError_t err = hipMalloc(&p, size);
+        if (err != hipSuccess) {
+            (void)hipGetLastError();
+            camel_hip_pool_trim();
+            err = hipMalloc(&p, size);
+        }
+        if (err != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(CAMEL_HIP_ERR_OOM, "camel_hip_malloc: out of device memory for " +
+                                               std::to_string(bytes) + " bytes");
+        }
+        *ptr = p;
+    }
+    s.live[*ptr] = size;
+    s.in_use += size;
+    return ok();
+}
+
+int camel_hip_free(void *ptr) {
+    if (!ptr) return ok();
+    CAMEL_LOCK();
+    State &s = state();
+    auto it = s.live.find(ptr);
+    if (it == s.live.end()) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_free: unknown pointer");
+    size_t size = it->second;
+    s.live.erase(it);
+    s.in_use -= size;
+    // Work already enqueued on the single stream may still read the block; a
+    // later allocation reuses it only through that same stream, so stream
+    // order keeps the reuse safe without a synchronisation here.
+    s.free_lists[size].push_back(ptr);
+    s.cached += size;
+    return ok();
+}
+
+int camel_hip_pool_trim(void) {
+    CAMEL_LOCK();
+    State &s = state();
+    if (!s.initialised) return ok();
+    CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize"));
+    for (auto &kv : s.free_lists) {
+        for (void *p : kv.second) (void)hipFree(p);
+        kv.second.clear();
+    }
+    s.cached = 0;
+    return ok();
+}
+
+int camel_hip_pool_stats(size_t *in_use, size_t *cached) {
+    CAMEL_LOCK();
+    if (in_use) *in_use = state().in_use;
+    if (cached) *cached = state().cached;
+    return ok();
+}
+
+int camel_hip_h2d(void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return ok();
+    if (!dst || !src) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_h2d: null pointer");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()),
+                              "hipMemcpyAsync(H2D)"));
+    CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+    return ok();
+}
+
+int camel_hip_d2h(void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return ok();
+    if (!dst || !src) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_d2h: null pointer");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream()),
+                              "hipMemcpyAsync(D2H)"));
+    CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+    return ok();
+}
+
+int camel_hip_d2d(void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return ok();
+    if (!dst || !src) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_d2d: null pointer");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream()),
+                              "hipMemcpyAsync(D2D)"));
+    return ok();
+}
+
+int camel_hip_fill(int dtype, void *out, int64_t n, double value) {
+    if (!valid_dtype(dtype)) return fail(CAMEL_HIP_ERR_DTYPE, "camel_hip_fill: unknown dtype");
+    if (n < 0) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_fill: negative size");
+    if (n == 0) return ok();
+    if (!out) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_fill: null output");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    if (dtype == CAMEL_DT_F32 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+        hipLaunchKernelGGL(fill_f32_kernel, dim3(grid_for(n / 4 + 1, 256)), dim3(256), 0, stream(),
+                           static_cast<float4 *>(out), static_cast<float *>(out), n, (float)value);
+        CAMEL_RETURN_IF(check_launch("fill_f32_kernel"));
+    } else {
+        hipLaunchKernelGGL(fill_generic_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream(),
+                           dtype, out, n, value);
+        CAMEL_RETURN_IF(check_launch("fill_generic_kernel"));
+    }
+    return ok();
+}
+
+int camel_hip_eye(float *out, int64_t n) {
+    if (n < 0) return fail(CAMEL_HIP_ERR_ARG, "eye size cannot be negative");
+    if (n == 0) return ok();
+    if (!out) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_eye: null output");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    hipLaunchKernelGGL(eye_kernel, dim3(grid_for(n * n, 256)), dim3(256), 0, stream(), out, n);
+    CAMEL_RETURN_IF(check_launch("eye_kernel"));
+    return ok();
+}
+
+int camel_hip_arange(int64_t *out, int64_t start, int64_t step, int64_t count) {
+    if (step == 0) return fail(CAMEL_HIP_ERR_ARG, "range step cannot be zero");
+    if (count < 0) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_arange: negative count");
+    if (count == 0) return ok();
+    if (!out) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_arange: null output");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    hipLaunchKernelGGL(arange_kernel, dim3(grid_for(count, 256)), dim3(256), 0, stream(), out,
+                       start, step, count);
+    CAMEL_RETURN_IF(check_launch("arange_kernel"));
+    return ok();
+}
+
+int camel_hip_event_create(void **event) {
+    if (!event) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_event_create: null output");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    hipEvent_t e;
+    CAMEL_RETURN_IF(check_hip(hipEventCreate(&e), "hipEventCreate"));
+    *event = (void *)e;
+    return ok();
+}
+
+int camel_hip_event_record(void *event) {
+    if (!event) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_event_record: null event");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(check_hip(hipEventRecord((hipEvent_t)event, stream()), "hipEventRecord"));
+    return ok();
+}
+
+int camel_hip_event_elapsed_ms(void *start, void *stop, float *ms) {
+    if (!start || !stop || !ms) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_event_elapsed_ms: null");
+    CAMEL_LOCK();
+    CAMEL_RETURN_IF(check_hip(hipEventSynchronize((hipEvent_t)stop), "hipEventSynchronize"));
+    CAMEL_RETURN_IF(
+        check_hip(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop), "hipEventElapsed"));
+    return ok();
+}
+
+int camel_hip_event_destroy(void *event) {
+    if (!event) return ok();
+    CAMEL_LOCK();
+    CAMEL_RETURN_IF(check_hip(hipEventDestroy((hipEvent_t)event), "hipEventDestroy"));
+    return ok();
+}
+
+} // extern "C"

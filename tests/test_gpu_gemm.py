@@ -1,0 +1,107 @@
+"""GPU parity of the MFMA fp32 GEMM (tensor:matmul / dense) against the CPU oracle.
+
+Tolerance (the north star's GEMM bar, stated per element): |C_gpu - C_ref| <=
+1e-5 * sqrt(K) * sum_k |A_ik| |B_kj|; the oracle accumulates in fp64 in k
+order exactly as operators.cpp:757-766.  Full-size shapes are checked on a
+row slab computed by the oracle plus size-independent identities.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from camel_amd import _hip as H
+from camel_amd import datagen as D
+from oracle import ffi as O
+from tests import hipkit as K
+
+pytestmark = pytest.mark.gpu
+
+P = C.c_void_p
+
+
+def _ab(M, N, Kd, seed):
+    a = D.uniform(seed, (M, Kd), -1.0, 1.0)
+    b = D.uniform(seed + 1, (Kd, N), -1.0, 1.0)
+    return a, b
+
+
+@pytest.mark.parametrize("M,N,Kd", [
+    (256, 256, 256),            # config 1
+    (1, 1, 1), (33, 17, 65), (7, 300, 5), (64, 64, 64), (100, 36, 1000),
+    (130, 258, 190),            # ragged edges on every tile shape
+    (1024, 10, 1024),           # MLP last layer (N=10, unaligned rows)
+    (512, 10, 128), (16, 512, 777), (31, 40, 12),
+])
+def test_sgemm_matches_oracle(M, N, Kd):
+    a, b = _ab(M, N, Kd, 0x1000 + M * 7 + N * 13 + Kd)
+    ref = O.matmul(a, b)
+    got = K.sgemm(a, b)
+    ok, worst = K.gemm_tol_ok(got, ref, a, b)
+    assert ok, f"worst error / bound = {worst}"
+
+
+def test_sgemm_zero_k_gives_zeros():
+    a = np.zeros((5, 0), np.float32)
+    b = np.zeros((0, 7), np.float32)
+    da, db = K.empty(4), K.empty(4)
+    dc = K.dev(np.full((5, 7), 3.0, np.float32))
+    H.call("camel_hip_sgemm", P(da.ptr), P(db.ptr), P(dc.ptr), 5, 7, 0, None, 0)
+    out = K.host(dc, np.float32, (5, 7))
+    assert np.array_equal(out, O.matmul(a, b))
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1024, 1024, 784), (1024, 1024, 1024), (512, 128, 9216)])
+def test_dense_bias_relu_matches_oracle(M, N, Kd):
+    a, w = _ab(M, N, Kd, 0x2000 + Kd)
+    bias = D.uniform(0x2100 + N, (N,), -0.5, 0.5)
+    ref = O.dense(a, w, bias, True)
+    got = K.sgemm(a, w, bias, H.EPI_BIAS | H.EPI_RELU)
+    ok, worst = K.gemm_tol_ok(got, ref, a, w)
+    assert ok, f"worst error / bound = {worst}"
+    # relu keeps the sign of zero: negatives become -0.0, never +0.0
+    neg = (ref < 0) | ((ref == 0) & np.signbit(ref))
+    assert np.all(np.signbit(got[(got == 0) & neg]))
+
+
+@pytest.mark.parametrize("n", [1024, 2048, 4096])
+def test_square_gemm_row_slab(n):
+    a, b = _ab(n, n, n, D.SEED_GEMM + n)
+    got = K.sgemm(a, b)
+    rows = 32 if n <= 2048 else 16
+    ref = O.matmul_rows(a, b, 0, rows)
+    ok, worst = K.gemm_tol_ok(got[:rows], ref, a[:rows], b)
+    assert ok, f"worst error / bound = {worst}"
+    # last rows too (different tile, different XCD)
+    ref_tail = O.matmul_rows(a, b, n - 8, n)
+    ok, worst = K.gemm_tol_ok(got[n - 8:], ref_tail, a[n - 8:], b)
+    assert ok, f"tail worst error / bound = {worst}"
+
+
+def test_skinny_gemm_matches_oracle():
+    a, b = _ab(16, 4096, 4096, D.SEED_GEMM + 16)
+    got = K.sgemm(a, b)
+    ref = O.matmul(a, b)
+    ok, worst = K.gemm_tol_ok(got, ref, a, b)
+    assert ok, f"worst error / bound = {worst}"
+
+
+def test_identity_and_ones_closed_forms():
+    # A @ I = A exactly; ones @ ones = K exactly (tensor_smoke.cml:9-11 pattern)
+    a = D.uniform(7, (300, 260), -1, 1)
+    eye = np.eye(260, dtype=np.float32)
+    assert np.array_equal(K.sgemm(a, eye), a)
+    ones_a = np.ones((70, 333), np.float32)
+    ones_b = np.ones((333, 90), np.float32)
+    assert np.all(K.sgemm(ones_a, ones_b) == 333.0)
+
+
+def test_generic_matmul_int64_bool_is_exact():
+    a = (np.arange(6 * 5).reshape(6, 5) - 11).astype(np.int64)
+    b = (np.arange(5 * 4).reshape(5, 4) % 2).astype(np.uint8)
+    ref = O.matmul(a, b)
+    da, db = K.dev(a), K.dev(b)
+    dc = K.empty(ref.nbytes)
+    H.call("camel_hip_matmul_generic", H.DT_I64, P(da.ptr), H.DT_BOOL, P(db.ptr), H.DT_I64,
+           P(dc.ptr), 6, 4, 5)
+    assert np.array_equal(K.host(dc, np.int64, (6, 4)), ref)
