@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X tensor-module backend (one GPU).
+
+Headline (`value`): fp32 GEMM C = A.B at M=N=K=4096 (the
+size the north-star target is quoted on), GFLOP/s of the whole timed loop,
+inputs resident in HBM.  The `suite` object carries the other BASELINE
+configs measured the same way (MLP forward, GEMM sweep, conv2d, small CNN,
+elementwise and softmax bandwidth), each with its own roofline entry.
+
+Timing: W warmup steps, device sync, then exactly K steps between two HIP
+events on the library stream (the stream every kernel is launched on),
+device sync after.  `roofline.achieved` = algorithmic FLOP (or bytes) of the
+dominant kernel per launch / its average launch time from those events.
+
+The CPU baseline times the oracle (a loop-for-loop restatement of the
+reference's CPU kernels, single thread) on a bounded row slab of the same
+workload, on this host, in this run.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite]
+       [--no-cpu] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from camel_amd import _hip as H  # noqa: E402
+from camel_amd import datagen as D  # noqa: E402
+
+P = C.c_void_p
+METRIC = "fp32 GEMM/conv GFLOP/s + % MFMA peak; elementwise GB/s + % HBM peak, 1 GPU"
+PEAK_MFMA_F32_TFLOPS = 157.3  # MI355X dense fp32 matrix, vendor figure
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E, vendor figure
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.txt")
+
+
+def _traffic(key: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.txt)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
+def _progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _time_loop(fn, steps: int, warmup: int):
+    for _ in range(warmup):
+        fn()
+    H.sync()
+    t = H.Timer()
+    wall0 = time.perf_counter()
+    t.begin()
+    for _ in range(steps):
+        fn()
+    ms = t.end()
+    H.sync()
+    wall = time.perf_counter() - wall0
+    return ms / steps, wall
+
+
+def sgemm_call(da, db, dc, M, N, K, dbias=None, flags=0):
+    return lambda: H.call("camel_hip_sgemm", P(da.ptr), P(db.ptr), P(dc.ptr), M, N, K,
+                          P(dbias.ptr) if dbias is not None else None, flags)
+
+
+def roofline_mfma(flop: float, ms: float, traffic=None):
+    ach = flop / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_MFMA_F32_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_F32_TFLOPS, 4), "traffic": traffic}
+
+
+def roofline_hbm(nbytes: float, ms: float, traffic=None):
+    ach = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic}
+
+
+# ---------------------------------------------------------------- workloads
+
+def wl_gemm(n_m, n_n, n_k, steps, warmup, seed=D.SEED_GEMM):
+    a = D.uniform(seed + n_m, (n_m, n_k), -1.0, 1.0)
+    b = D.uniform(seed + n_m + 1, (n_k, n_n), -1.0, 1.0)
+    da, db, dc = H.to_device(a), H.to_device(b), H.DeviceBuffer(n_m * n_n * 4)
+    ms, wall = _time_loop(sgemm_call(da, db, dc, n_m, n_n, n_k), steps, warmup)
+    flop = 2.0 * n_m * n_n * n_k
+    return {"ms": ms, "wall_s": wall, "flop": flop, "value": flop / (ms * 1e-3) / 1e9,
+            "unit": "GFLOP/s", "a": a, "b": b}
+
+
+def wl_skinny(steps, warmup):
+    # M=16, N=K=4096: B (64 MiB) fits the 256 MiB MALL, so rotate 6 buffer sets
+    # (>= 400 MiB) to measure HBM rather than cache.
+    sets = []
+    for s in range(6):
+        a = D.uniform(D.SEED_GEMM + 16 + 10 * s, (16, 4096), -1.0, 1.0)
+        b = D.uniform(D.SEED_GEMM + 17 + 10 * s, (4096, 4096), -1.0, 1.0)
+        sets.append((H.to_device(a), H.to_device(b), H.DeviceBuffer(16 * 4096 * 4)))
+    it = [0]
+
+    def step():
+        da, db, dc = sets[it[0] % len(sets)]
+        it[0] += 1
+        sgemm_call(da, db, dc, 16, 4096, 4096)()
+
+    ms, wall = _time_loop(step, steps, warmup)
+    flop = 2.0 * 16 * 4096 * 4096
+    nbytes = 4.0 * (16 * 4096 + 4096 * 4096 + 16 * 4096)
+    return {"ms": ms, "flop": flop, "bytes": nbytes}
+
+
+def wl_mlp(steps, warmup):
+    """dense 784->1024->1024->10 (+relu) then row softmax, batch 1024."""
+    B = 1024
+    dims = [784, 1024, 1024, 10]
+    x = D.uniform(D.SEED_MLP, (B, dims[0]), 0.0, 1.0)
+    ws = [D.normal(D.SEED_MLP + 1 + i, (dims[i], dims[i + 1]), std=float(np.sqrt(1.0 / dims[i])))
+          for i in range(3)]
+    bs = [np.zeros(dims[i + 1], np.float32) for i in range(3)]
+    dx = H.to_device(x)
+    dws = [H.to_device(w) for w in ws]
+    dbs = [H.to_device(b) for b in bs]
+    acts = [H.DeviceBuffer(B * d * 4) for d in dims[1:]]
+    dp = H.DeviceBuffer(B * 10 * 4)
+
+    def step():
+        src = dx
+        for i in range(3):
+            flags = H.EPI_BIAS | (H.EPI_RELU if i < 2 else 0)
+            sgemm_call(src, dws[i], acts[i], B, dims[i + 1], dims[i], dbs[i], flags)()
+            src = acts[i]
+        H.call("camel_hip_softmax_rows", P(acts[2].ptr), P(dp.ptr), B, 10)
+
+    ms, wall = _time_loop(step, steps, warmup)
+    flop = sum(2.0 * B * dims[i] * dims[i + 1] for i in range(3))
+    return {"ms": ms, "flop": flop, "x": x, "ws": ws, "bs": bs, "dp": dp}
+
+
+def wl_conv(steps, warmup):
+    """conv2d 64x64x56x56 -> 128, 3x3, s1 p1, bias + relu."""
+    x = D.normal(D.SEED_CONV_X, (64, 64, 56, 56))
+    w = D.normal(D.SEED_CONV_W, (128, 64, 3, 3), std=float(np.sqrt(2.0 / (9 * 64))))
+    b = np.zeros(128, np.float32)
+    dx, dw, db = H.to_device(x), H.to_device(w), H.to_device(b)
+    dy = H.DeviceBuffer(64 * 128 * 56 * 56 * 4)
+    call = lambda: H.call("camel_hip_conv2d", P(dx.ptr), P(dw.ptr), P(db.ptr), P(dy.ptr), 64, 64,
+                          56, 56, 128, 3, 3, 1, 1, H.EPI_BIAS | H.EPI_RELU)
+    ms, wall = _time_loop(call, steps, warmup)
+    flop = 2.0 * (64 * 56 * 56) * 128 * (64 * 9)
+    return {"ms": ms, "flop": flop, "x": x, "w": w, "b": b}
+
+
+def wl_cnn(steps, warmup):
+    """small CNN forward, batch 512 (valid 3x3 convs, 2x2 pool)."""
+    B = 512
+    x = D.uniform(D.SEED_CNN, (B, 1, 28, 28), 0.0, 1.0)
+    w1 = D.normal(D.SEED_CNN + 1, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
+    w2 = D.normal(D.SEED_CNN + 2, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288)))
+    w3 = D.normal(D.SEED_CNN + 3, (9216, 128), std=float(np.sqrt(2.0 / 9216)))
+    w4 = D.normal(D.SEED_CNN + 4, (128, 10), std=float(np.sqrt(2.0 / 128)))
+    z = lambda n: H.to_device(np.zeros(n, np.float32))
+    dx, d1, d2, d3, d4 = (H.to_device(t) for t in (x, w1, w2, w3, w4))
+    b1, b2, b3, b4 = z(32), z(64), z(128), z(10)
+    a1 = H.DeviceBuffer(B * 32 * 26 * 26 * 4)
+    a2 = H.DeviceBuffer(B * 64 * 24 * 24 * 4)
+    a3 = H.DeviceBuffer(B * 64 * 12 * 12 * 4)
+    a4 = H.DeviceBuffer(B * 128 * 4)
+    a5 = H.DeviceBuffer(B * 10 * 4)
+    dp = H.DeviceBuffer(B * 10 * 4)
+    EPI = H.EPI_BIAS | H.EPI_RELU
+
+    def step():
+        H.call("camel_hip_conv2d", P(dx.ptr), P(d1.ptr), P(b1.ptr), P(a1.ptr), B, 1, 28, 28, 32, 3, 3, 1, 0, EPI)
+        H.call("camel_hip_conv2d", P(a1.ptr), P(d2.ptr), P(b2.ptr), P(a2.ptr), B, 32, 26, 26, 64, 3, 3, 1, 0, EPI)
+        H.call("camel_hip_maxpool2d", P(a2.ptr), P(a3.ptr), B, 64, 24, 24, 2, 2, 2)
+        sgemm_call(a3, d3, a4, B, 128, 9216, b3, EPI)()
+        sgemm_call(a4, d4, a5, B, 10, 128, b4, H.EPI_BIAS)()
+        H.call("camel_hip_softmax_rows", P(a5.ptr), P(dp.ptr), B, 10)
+
+    ms, wall = _time_loop(step, steps, warmup)
+    flop = 2.0 * B * (26 * 26 * 32 * 9 + 24 * 24 * 64 * 288 + 9216 * 128 + 128 * 10)
+    return {"ms": ms, "flop": flop}
+
+
+def _big_input(seed, n, lo=-1.0, hi=1.0):
+    # 1 GiB buffers: generate 16 Mi seeded values and tile them (bandwidth is
+    # independent of the values; the buffers still exceed the 256 MiB MALL).
+    base = D.uniform(seed, (1 << 24,), lo, hi)
+    return np.tile(base, n // base.size)
+
+
+def wl_eltwise(steps, warmup):
+    n = 1 << 28
+    a = _big_input(D.SEED_ELT, n)
+    b = _big_input(D.SEED_ELT + 1, n)
+    da, db, dc = H.to_device(a), H.to_device(b), H.DeviceBuffer(n * 4)
+    del a, b
+    out = {}
+    for name, op in (("add", H.OP_ADD), ("mul", H.OP_MUL)):
+        call = lambda op=op: H.call("camel_hip_binary", op, H.DT_F32, P(da.ptr), H.DT_F32, P(db.ptr),
+                                    H.DT_F32, P(dc.ptr), n)
+        ms, _ = _time_loop(call, steps, warmup)
+        out[name] = {"ms": ms, "bytes": 12.0 * n}
+    call = lambda: H.call("camel_hip_relu", P(da.ptr), P(dc.ptr), n)
+    ms, _ = _time_loop(call, steps, warmup)
+    out["relu"] = {"ms": ms, "bytes": 8.0 * n}
+    return out
+
+
+def wl_softmax(steps, warmup):
+    rows, cols = 262144, 1024
+    base = D.normal(D.SEED_ELT + 2, (1 << 24,))
+    x = np.tile(base, rows * cols // base.size)
+    dx, dy = H.to_device(x), H.DeviceBuffer(rows * cols * 4)
+    del x
+    call = lambda: H.call("camel_hip_softmax_rows", P(dx.ptr), P(dy.ptr), rows, cols)
+    ms, _ = _time_loop(call, steps, warmup)
+    return {"ms": ms, "bytes": 8.0 * rows * cols}
+
+
+# ------------------------------------------------------------- CPU baseline
+
+def cpu_baseline_gemm(a, b, budget_s: float = 12.0):
+    """Oracle ijk matmul (reference operators.cpp:757-766) on a row slab, 1 thread."""
+    from oracle import ffi as O  # the CPU baseline leg is the only bench user of the oracle
+    M, K = a.shape
+    N = b.shape[1]
+    rows, spent = 0, 0.0
+    t0 = time.perf_counter()
+    O.matmul_rows(a, b, 0, 1)  # warm
+    per_row = time.perf_counter() - t0
+    target = max(1, min(M, int(budget_s / max(per_row, 1e-6))))
+    t0 = time.perf_counter()
+    O.matmul_rows(a, b, 0, target)
+    spent = time.perf_counter() - t0
+    rows = target
+    gflops = 2.0 * rows * N * K / spent / 1e9
+    return {"value": round(gflops, 4), "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"rows 0-{rows - 1} of the {M}x{N}x{K} fp32 matmul through the oracle "
+                      f"(ijk, fp64 accumulate, per-element dtype dispatch), {spent:.1f} s on 1 of "
+                      f"{os.cpu_count()} host cores"}
+
+
+# ------------------------------------------------------------------- main
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-suite", action="store_true", help="headline GEMM only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--workload", default="gemm4096",
+                    choices=["gemm4096", "mlp", "conv2d", "cnn", "eltwise", "softmax", "skinny"])
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only; multi-GPU runs are not supported "
+              "(use --gpus 1)", file=sys.stderr)
+        return 2
+
+    H.call("camel_hip_init", 0)
+    steps, warmup = args.steps, args.warmup
+
+    if args.workload != "gemm4096":
+        # single-workload mode (used for profiling one kernel at a time)
+        fn = {"mlp": wl_mlp, "conv2d": wl_conv, "cnn": wl_cnn, "eltwise": wl_eltwise,
+              "softmax": wl_softmax, "skinny": wl_skinny}[args.workload]
+        res = fn(steps, warmup)
+        keep = {k: v for k, v in res.items() if isinstance(v, (int, float, dict))}
+        print(json.dumps({"workload": args.workload, **keep}))
+        return 0
+
+    g = wl_gemm(4096, 4096, 4096, steps, warmup)
+    _progress(f"sgemm 4096^3: {g['ms']:.4f} ms/step, {g['value']:.0f} GFLOP/s")
+    line = {
+        "metric": METRIC,
+        "value": round(g["value"], 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(g["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded SplitMix64 U(-1,1), generated on host, resident in HBM)",
+        "config": {"workload": "sgemm M=N=K=4096 (BASELINE config 3)", "M": 4096, "N": 4096,
+                   "K": 4096, "layout": "row-major contiguous", "parallelism": "single GPU"},
+        "roofline": roofline_mfma(g["flop"], g["ms"], _traffic("sgemm_4096")),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_gemm(g["a"], g["b"])
+        _progress(f"cpu baseline: {line['cpu_baseline']['value']} GFLOP/s")
+    del g
+
+    if not args.no_suite:
+        suite = {}
+        s_steps, s_warm = max(5, steps // 5), 2
+        for n in (1024, 2048, 8192):
+            r = wl_gemm(n, n, n, s_steps if n < 8192 else 5, s_warm)
+            suite[f"sgemm_{n}"] = {"value": round(r["value"], 1), "unit": "GFLOP/s",
+                                   "ms": round(r["ms"], 4),
+                                   "roofline": roofline_mfma(r["flop"], r["ms"])}
+        r = wl_skinny(s_steps * 4, s_warm)
+        suite["sgemm_16x4096x4096"] = {
+            "value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1), "unit": "GFLOP/s",
+            "ms": round(r["ms"], 4), "roofline": roofline_hbm(r["bytes"], r["ms"])}
+        r = wl_mlp(s_steps * 2, s_warm)
+        suite["mlp_forward"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
+                                "unit": "GFLOP/s", "ms": round(r["ms"], 4),
+                                "roofline": roofline_mfma(r["flop"], r["ms"])}
+        r = wl_conv(s_steps, s_warm)
+        suite["conv2d_3x3"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
+                               "unit": "GFLOP/s", "ms": round(r["ms"], 4),
+                               "roofline": roofline_mfma(r["flop"], r["ms"], _traffic("conv2d"))}
+        r = wl_cnn(s_steps, s_warm)
+        suite["cnn_forward"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
+                                "unit": "GFLOP/s", "ms": round(r["ms"], 4),
+                                "roofline": roofline_mfma(r["flop"], r["ms"])}
+        e = wl_eltwise(s_steps, s_warm)
+        for name, r in e.items():
+            suite[f"eltwise_{name}"] = {"value": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1),
+                                        "unit": "GB/s", "ms": round(r["ms"], 4),
+                                        "roofline": roofline_hbm(r["bytes"], r["ms"],
+                                                                 _traffic(f"eltwise_{name}"))}
+        r = wl_softmax(s_steps, s_warm)
+        suite["softmax_262144x1024"] = {"value": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1),
+                                        "unit": "GB/s", "ms": round(r["ms"], 4),
+                                        "roofline": roofline_hbm(r["bytes"], r["ms"],
+                                                                 _traffic("softmax"))}
+        line["suite"] = suite
+        for k, v in suite.items():
+            _progress(f"{k}: {v['value']} {v['unit']} ({100 * v['roofline']['frac']:.1f}% of peak)")
+
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -7,9 +7,11 @@ namespace {
 constexpr int TT = 32; // transpose tile edge
 
 // tensorTranspose2D (runtime.cpp:704-720) copies each element through
-// getAsDouble/setFromDouble; int64 values therefore pass through a double.
-// fp32 and bool round-trip exactly, so those move their raw bits.
-template <class T, bool VIA_DOUBLE>
+// getAsDouble/setFromDouble: int64 values pass through a double and bool
+// bytes are normalised to 0/1; fp32 round-trips exactly (raw bits move).
+enum { COPY_RAW = 0, COPY_I64_VIA_DOUBLE = 1, COPY_BOOL_NORMALISE = 2 };
+
+template <class T, int MODE>
 __global__ __launch_bounds__(TT * 8) void transpose_kernel(const T *__restrict__ x,
                                                            T *__restrict__ y, int64_t rows,
                                                            int64_t cols) {
@@ -25,7 +27,8 @@ __global__ __launch_bounds__(TT * 8) void transpose_kernel(const T *__restrict__
         const int64_t c = c0 + k, r = r0 + tx; // output row c, column r
         if (r < rows && c < cols) {
             T v = tile[tx][k];
-            if constexpr (VIA_DOUBLE) v = (T)double_to_i64_x86((double)v);
+            if constexpr (MODE == COPY_I64_VIA_DOUBLE) v = (T)double_to_i64_x86((double)v);
+            if constexpr (MODE == COPY_BOOL_NORMALISE) v = v != 0 ? 1 : 0;
             y[c * rows + r] = v;
         }
     }
@@ -96,13 +99,13 @@ int camel_hip_transpose2d(int dt, const void *x, void *y, int64_t rows, int64_t 
     CAMEL_INIT_OR_RETURN();
     dim3 grid((unsigned)((cols + TT - 1) / TT), (unsigned)((rows + TT - 1) / TT)), block(TT * 8);
     if (dt == CAMEL_DT_F32)
-        hipLaunchKernelGGL((transpose_kernel<float, false>), grid, block, 0, stream(),
+        hipLaunchKernelGGL((transpose_kernel<float, COPY_RAW>), grid, block, 0, stream(),
                            static_cast<const float *>(x), static_cast<float *>(y), rows, cols);
     else if (dt == CAMEL_DT_I64)
-        hipLaunchKernelGGL((transpose_kernel<int64_t, true>), grid, block, 0, stream(),
+        hipLaunchKernelGGL((transpose_kernel<int64_t, COPY_I64_VIA_DOUBLE>), grid, block, 0, stream(),
                            static_cast<const int64_t *>(x), static_cast<int64_t *>(y), rows, cols);
     else
-        hipLaunchKernelGGL((transpose_kernel<uint8_t, false>), grid, block, 0, stream(),
+        hipLaunchKernelGGL((transpose_kernel<uint8_t, COPY_BOOL_NORMALISE>), grid, block, 0, stream(),
                            static_cast<const uint8_t *>(x), static_cast<uint8_t *>(y), rows, cols);
     CAMEL_RETURN_IF(check_launch("transpose_kernel"));
     return ok();

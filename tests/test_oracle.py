@@ -1,0 +1,341 @@
+"""Pins the CPU oracle (oracle/tensor_oracle.c) before it is trusted as the checker.
+
+Each check is chosen so that a plausible restatement mistake fails it:
+fp32 instead of fp64 accumulation, a reversed k loop, a transposed operand,
+fmaxf-style relu, a wrong tie or NaN rule in max/argmax, a wrong promotion.
+References used: closed forms, IEEE fp32 arithmetic as numpy implements it,
+Python's libm (the same glibc the reference calls), exact rational brute force,
+and the reference's own self-checking program test/run/nn/tensor_smoke.cml.
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from camel_amd import datagen as D
+from oracle import ffi as O
+
+F = np.float32
+
+
+# ---------------------------------------------------------------- matmul (a3)
+
+def test_matmul_identity_and_ones():
+    a = D.uniform(11, (17, 23), -1, 1)
+    assert np.array_equal(O.matmul(a, np.eye(23, dtype=F)), a)
+    assert np.array_equal(O.matmul(np.eye(17, dtype=F), a), a)
+    assert np.all(O.matmul(np.ones((4, 9), F), np.ones((9, 5), F)) == 9.0)
+
+
+def test_matmul_accumulates_in_fp64():
+    # fp64: 2^24 + 1 - 2^24 = 1; fp32 sequential accumulation would give 0.
+    a = np.array([[2.0 ** 24, 1.0, -(2.0 ** 24)]], F)
+    assert O.matmul(a, np.ones((3, 1), F))[0, 0] == 1.0
+
+
+def test_matmul_k_order_is_ascending():
+    # Ascending: (2^53 + 1) rounds to 2^53, minus 2^53 -> 0.  Descending: 1.
+    a = np.array([[2.0 ** 53, 1.0, -(2.0 ** 53)]], F)
+    assert O.matmul(a, np.ones((3, 1), F))[0, 0] == 0.0
+
+
+def test_matmul_not_transposed_exact_rationals():
+    rng = np.random.default_rng(5)
+    a = rng.integers(-8, 9, size=(5, 7)).astype(F)
+    b = rng.integers(-8, 9, size=(7, 3)).astype(F)
+    exact = [[sum(Fraction(int(a[i, k])) * Fraction(int(b[k, j])) for k in range(7))
+              for j in range(3)] for i in range(5)]
+    got = O.matmul(a, b)
+    assert all(Fraction(float(got[i, j])) == exact[i][j] for i in range(5) for j in range(3))
+    assert not np.array_equal(got.T, got[:3, :5])  # a transposed product would differ
+
+
+def test_matmul_promotes_dtypes():
+    a = np.arange(6, dtype=np.int64).reshape(2, 3)
+    b = np.ones((3, 2), np.uint8)
+    out = O.matmul(a, b)
+    assert out.dtype == np.int64 and np.array_equal(out, a @ b.astype(np.int64))
+    assert O.matmul(a, np.ones((3, 2), F)).dtype == F
+
+
+def test_tensor_smoke_closed_forms():
+    # test/run/nn/tensor_smoke.cml:9-15
+    c = O.matmul(np.ones((2, 2), F), np.eye(2, dtype=F))
+    d = O.binary_scalar(O.ADD, c, 2.0, O.F32)
+    assert np.all(d == 3.0) and O.sum_all(d) == 12.0
+    e = O.concat(np.array([[1.0, 2.0]], F), np.array([[3.0, 4.0]], F), 0)
+    assert np.array_equal(e, [[1, 2], [3, 4]])
+    assert np.array_equal(O.transpose2d(e), [[1, 3], [2, 4]])
+
+
+# ------------------------------------------------------ elementwise (a4-a6)
+
+SPECIALS = np.array([0.0, -0.0, 1.0, -1.0, 1.5, -2.75, np.inf, -np.inf, np.nan, 1e-45, -1e-45,
+                     1.17549435e-38, 3.4028235e38, -3.4028235e38, 0.1, 3.0, 7e-39, 1e30],
+                    dtype=F)
+
+
+def _pairs():
+    a = np.repeat(SPECIALS, SPECIALS.size)
+    b = np.tile(SPECIALS, SPECIALS.size)
+    return a, b
+
+
+@pytest.mark.parametrize("op,npop", [(O.ADD, np.add), (O.SUB, np.subtract), (O.MUL, np.multiply)])
+def test_binary_f32_equals_ieee_fp32(op, npop):
+    a, b = _pairs()
+    got = O.binary(op, a, b)
+    with np.errstate(all="ignore"):
+        want = npop(a, b)
+    assert got.dtype == F
+    assert np.array_equal(got.view(np.uint32)[~np.isnan(want)], want.view(np.uint32)[~np.isnan(want)])
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+
+
+def test_divide_equals_ieee_and_throws_on_zero():
+    a, b = _pairs()
+    keep = b != 0
+    got = O.binary(O.DIV, a[keep], b[keep])
+    with np.errstate(all="ignore"):
+        want = a[keep] / b[keep]
+    ok = ~np.isnan(want)
+    assert np.array_equal(got.view(np.uint32)[ok], want.view(np.uint32)[ok])
+    with pytest.raises(O.OracleError, match="Division by zero"):
+        O.binary(O.DIV, np.ones(3, F), np.array([1.0, 0.0, 2.0], F))
+    with pytest.raises(O.OracleError, match="Division by zero"):
+        O.binary_scalar(O.DIV, np.ones(3, F), 0.0, O.F32)
+
+
+def test_scalar_ops_round_once_from_double():
+    # 0.1 is a double scalar: x + 0.1 rounds (double)x + 0.1 once to fp32.
+    x = np.array([1.0, 3.0, 1e-8, 16777216.0], F)
+    got = O.binary_scalar(O.ADD, x, 0.1, O.F32)
+    want = np.array([F(float(v) + 0.1) for v in x], F)
+    assert np.array_equal(got, want)
+    # The scalar stays double: 1 + (2^-24 + 2^-50) rounds up to 1 + 2^-23, while
+    # the fp32 add of fl32(s) = 2^-24 is a tie that rounds to even (1.0).
+    s = 2.0 ** -24 + 2.0 ** -50
+    assert O.binary_scalar(O.ADD, np.array([1.0], F), s, O.F32)[0] == F(1.0 + 2.0 ** -23)
+    assert F(1.0) + F(s) == F(1.0)
+    left = O.binary_scalar(O.SUB, x, 1.0, O.F32, side=1)
+    assert np.array_equal(left, np.array([F(1.0 - float(v)) for v in x], F))
+
+
+def test_int64_binary_goes_through_double():
+    big = np.array([2 ** 53 + 1, 5, -7], np.int64)
+    one = np.array([0, 2, 3], np.int64)
+    got = O.binary(O.ADD, big, one)
+    assert got.dtype == np.int64
+    assert got[0] == 2 ** 53  # (double)(2^53+1) rounds to 2^53
+    assert list(got[1:]) == [7, -4]
+
+
+def test_promotion_table():
+    assert O.promote(O.F32, O.I64) == O.F32
+    assert O.promote(O.I64, O.BOOL) == O.I64
+    assert O.promote(O.BOOL, O.BOOL) == O.BOOL
+    assert O.binary_out_dtype(O.DIV, O.I64, O.I64) == O.F32
+    assert O.binary_out_dtype(O.POW, O.BOOL, O.BOOL) == O.F32
+    b = O.binary(O.ADD, np.array([1, 0, 1], np.uint8), np.array([1, 0, 0], np.uint8))
+    assert b.dtype == np.uint8 and list(b) == [1, 0, 1]
+
+
+def test_pow_matches_libm():
+    x = np.array([2.0, 0.5, 9.0, 1.1, 0.0], F)
+    got = O.binary_scalar(O.POW, x, 2.5, O.F32)
+    assert np.array_equal(got, np.array([F(math.pow(float(v), 2.5)) for v in x], F))
+
+
+@pytest.mark.parametrize("op,npop", [(O.LT, np.less), (O.LE, np.less_equal), (O.GT, np.greater),
+                                     (O.GE, np.greater_equal), (O.EQ, np.equal)])
+def test_compare_matches_ieee(op, npop):
+    a, b = _pairs()
+    assert np.array_equal(O.compare(op, a, b), npop(a, b).astype(np.uint8))
+    assert np.array_equal(O.compare_scalar(op, a, 1.0), npop(a, F(1.0)).astype(np.uint8))
+
+
+# --------------------------------------------------------------- relu (a7)
+
+def test_relu_idiom_sign_of_zero_nan_inf():
+    x = np.array([-3.0, -0.0, 0.0, 2.5, np.nan, -np.inf, np.inf, -1e-45], F)
+    y = O.relu(x)
+    assert y[0] == 0 and np.signbit(y[0])       # -3 -> -0.0 (fmaxf would give +0.0)
+    assert y[1] == 0 and np.signbit(y[1])       # -0.0 -> -0.0
+    assert y[2] == 0 and not np.signbit(y[2])   # +0.0 -> +0.0
+    assert y[3] == 2.5
+    assert np.isnan(y[4]) and np.isnan(y[5])    # NaN -> NaN, -inf * 0 -> NaN
+    assert y[6] == np.inf
+    assert y[7] == 0 and np.signbit(y[7])
+
+
+# ----------------------------------------------------------- reductions
+
+def test_max_argmax_first_strict_rule():
+    x = np.array([[1.0, 3.0, 3.0, 2.0],
+                  [np.nan, 5.0, 1.0, 9.0],
+                  [1.0, np.nan, 2.0, 0.5],
+                  [-0.0, 0.0, -1.0, -0.0],
+                  [0.0, -0.0, -1.0, -2.0]], F)
+    m = O.max_axis(x, 1)
+    am = O.argmax_axis(x, 1)
+    assert list(am) == [1, 0, 2, 0, 0]
+    assert m[0] == 3.0 and np.isnan(m[1]) and m[2] == 2.0
+    assert m[3] == 0 and np.signbit(m[3]) and not np.signbit(m[4])
+    assert list(O.argmax_axis(x.T.copy(), 0)) == [1, 0, 2, 0, 0]
+    assert np.array_equal(O.max_axis(x.T.copy(), -2).view(np.uint32)[[0, 2, 3, 4]],
+                          m.view(np.uint32)[[0, 2, 3, 4]])
+
+
+def test_sum_axis_and_sum_are_fp64():
+    x = np.array([[2.0 ** 24, 1.0, -(2.0 ** 24), 1.0]], F)
+    assert O.sum_axis(x, 1)[0] == 2.0
+    assert O.sum_axis(x, -1)[0] == 2.0
+    assert O.sum_all(np.array([0.1, 0.2], F)) == float(F(0.1)) + float(F(0.2))
+    assert np.array_equal(O.sum_axis(np.ones((3, 4), F), 0), np.full(4, 3.0, F))
+    with pytest.raises(O.OracleError):
+        O.sum_axis(np.ones((2, 2), F), 2)
+
+
+def test_exp_log_match_libm_and_log_domain():
+    x = D.uniform(3, (200,), -20, 20)
+    assert np.array_equal(O.exp(x), np.array([F(math.exp(float(v))) for v in x], F))
+    p = np.abs(x) + F(0.01)
+    assert np.array_equal(O.log(p), np.array([F(math.log(float(v))) for v in p], F))
+    with pytest.raises(O.OracleError, match="positive"):
+        O.log(np.array([1.0, 0.0], F))
+    assert np.isnan(O.log(np.array([np.nan], F))[0])  # NaN <= 0 is false: no error
+
+
+# ------------------------------------------------------------ softmax (a8)
+
+def test_softmax_invariants_and_closed_forms():
+    x = D.normal(21, (64, 37))
+    p = O.softmax_rows(x)
+    ref = np.exp(x.astype(np.float64) - x.max(1, keepdims=True))
+    ref /= ref.sum(1, keepdims=True)
+    assert np.max(np.abs(p - ref) / np.maximum(ref, 1e-30)) <= 1e-6
+    assert np.max(np.abs(p.astype(np.float64).sum(1) - 1.0)) <= 1e-5
+    # uniform rows -> 1/k; a dominant logit -> one-hot
+    u = O.softmax_rows(np.full((2, 8), 4.0, F))
+    assert np.all(u == F(1.0) / F(8.0))
+    oh = O.softmax_rows(np.array([[0.0, -1000.0, -1000.0]], F))
+    assert list(oh[0]) == [1.0, 0.0, 0.0]
+    # shift invariance (x + 8 rounds, so within the softmax tolerance)
+    assert np.max(np.abs(O.softmax_rows(x + F(8.0)) - p) / p) <= 1e-5
+
+
+def test_softmax_composition_op_for_op():
+    # stable = x - bcast(max) must be formed in fp32 before exp (mnist.cml:19-20)
+    x = np.array([[1e8, 1e8 - 8.0, 0.0]], F)
+    p = O.softmax_rows(x)
+    e = np.array([F(math.exp(float(F(v - F(1e8))))) for v in x[0]], F)
+    s = F(sum(float(v) for v in e))
+    assert np.array_equal(p[0], e / s)
+
+
+# ------------------------------------------------------------- dense (a9)
+
+def test_dense_is_matmul_then_bias_then_relu():
+    x = D.uniform(31, (9, 13), -1, 1)
+    w = D.uniform(32, (13, 6), -1, 1)
+    b = D.uniform(33, (6,), -1, 1)
+    mm = O.matmul(x, w)
+    assert np.array_equal(O.dense(x, w, None, False), mm)
+    biased = (mm + b[None, :]).astype(F)  # numpy fp32 add == correctly rounded add
+    assert np.array_equal(O.dense(x, w, b, False), biased)
+    assert np.array_equal(O.dense(x, w, b, True).view(np.uint32), O.relu(biased).view(np.uint32))
+
+
+# ------------------------------------------------------------ conv2d (a10)
+
+def _im2col(x, KH, KW, stride, pad):
+    N, C, H, W = x.shape
+    OH, OW = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    xp = np.zeros((N, C, H + 2 * pad, W + 2 * pad), F)
+    xp[:, :, pad:pad + H, pad:pad + W] = x
+    cols = np.empty((N, OH, OW, C, KH, KW), F)
+    for kh in range(KH):
+        for kw in range(KW):
+            cols[:, :, :, :, kh, kw] = xp[:, :, kh:kh + stride * OH:stride,
+                                          kw:kw + stride * OW:stride].transpose(0, 2, 3, 1)
+    return cols.reshape(N * OH * OW, C * KH * KW), OH, OW
+
+
+@pytest.mark.parametrize("N,C,H,W,Co,k,stride,pad", [
+    (2, 3, 7, 6, 4, 3, 1, 1), (1, 1, 5, 5, 2, 3, 1, 0), (2, 2, 8, 9, 3, 3, 2, 1), (1, 4, 4, 4, 5, 1, 1, 0)])
+def test_conv2d_equals_im2col_matmul(N, C, H, W, Co, k, stride, pad):
+    x = D.normal(41, (N, C, H, W))
+    w = D.normal(42, (Co, C, k, k))
+    b = D.uniform(43, (Co,), -0.1, 0.1)
+    cols, OH, OW = _im2col(x, k, k, stride, pad)
+    mm = O.matmul(cols, w.reshape(Co, -1).T.copy())          # [N*OH*OW, Co]
+    want = (mm + b[None, :]).astype(F)
+    want = O.relu(want).reshape(N, OH, OW, Co).transpose(0, 3, 1, 2)
+    got = O.conv2d(x, w, b, True, stride, pad)
+    assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(want).view(np.uint32))
+
+
+def test_conv2d_brute_force_integers():
+    rng = np.random.default_rng(9)
+    x = rng.integers(-3, 4, size=(1, 2, 4, 5)).astype(F)
+    w = rng.integers(-3, 4, size=(3, 2, 3, 3)).astype(F)
+    got = O.conv2d(x, w, None, False, 1, 1)
+    for co in range(3):
+        for oh in range(4):
+            for ow in range(5):
+                s = 0
+                for c in range(2):
+                    for kh in range(3):
+                        for kw in range(3):
+                            ih, iw = oh + kh - 1, ow + kw - 1
+                            if 0 <= ih < 4 and 0 <= iw < 5:
+                                s += int(x[0, c, ih, iw]) * int(w[co, c, kh, kw])
+                assert got[0, co, oh, ow] == s
+
+
+# ----------------------------------------------------------- maxpool (a11)
+
+def test_maxpool_brute_force_and_ties():
+    x = D.normal(51, (2, 3, 6, 8))
+    got = O.maxpool2d(x, 2, 2)
+    want = x.reshape(2, 3, 3, 2, 4, 2).max(axis=(3, 5))
+    assert np.array_equal(got, want)
+    z = np.array([[[[-0.0, 0.0], [0.0, -0.0]]]], F)
+    assert np.signbit(O.maxpool2d(z)[0, 0, 0, 0])          # first element wins ties
+    n = np.array([[[[1.0, np.nan], [3.0, 2.0]]]], F)
+    assert O.maxpool2d(n)[0, 0, 0, 0] == 3.0                 # NaN never replaces
+    n0 = np.array([[[[np.nan, 5.0], [3.0, 2.0]]]], F)
+    assert np.isnan(O.maxpool2d(n0)[0, 0, 0, 0])             # NaN as first element stays
+
+
+# ------------------------------------------------------- layout (a13)
+
+def test_transpose_concat():
+    x = D.uniform(61, (5, 7), -1, 1)
+    assert np.array_equal(O.transpose2d(x), x.T)
+    big = np.array([[2 ** 53 + 1, 3]], np.int64)
+    assert O.transpose2d(big)[0, 0] == 2 ** 53  # element copy goes through double
+    a = np.arange(24, dtype=np.int64).reshape(2, 3, 4)
+    b = np.arange(16, dtype=np.int64).reshape(2, 2, 4) + 100
+    assert np.array_equal(O.concat(a, b, 1), np.concatenate([a, b], 1))
+
+
+# ------------------------------------------------------- input generator
+
+def test_splitmix64_known_answers():
+    # Published first outputs of SplitMix64 seeded with 0.
+    assert O.lib().ot_splitmix64(0, 0) == 0xE220A8397B1DCDAF
+    assert O.lib().ot_splitmix64(0, 1) == 0x6E789E6AA1B965F4
+    assert O.lib().ot_splitmix64(0, 2) == 0x06C45D188009454F
+    assert [int(v) for v in D.splitmix64(0, 0, 3)] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4,
+                                                       0x06C45D188009454F]
+
+
+def test_uniform_generator_matches_c_and_is_exact():
+    n = 1000
+    c = np.empty(n, F)
+    O.lib().ot_fill_uniform(O.ptr(c), n, 123, F(-1.0), F(1.0))
+    assert np.array_equal(D.uniform(123, (n,), -1.0, 1.0), c)
+    u = D.uniform(5, (4096,))
+    assert u.min() >= 0 and u.max() < 1 and np.all(u * F(2 ** 24) == np.floor(u * F(2 ** 24)))
