@@ -222,6 +222,17 @@ def wl_eltwise(steps, warmup):
     return out
 
 
+def wl_copy(steps, warmup):
+    """1 GiB device-to-device copy: the known-size transfer that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters (reads 1 GiB, writes 1 GiB per launch)."""
+    n = 1 << 28
+    da, db = H.DeviceBuffer(n * 4), H.DeviceBuffer(n * 4)
+    H.call("camel_hip_fill", H.DT_F32, P(da.ptr), n, 1.0)
+    call = lambda: H.call("camel_hip_d2d", P(db.ptr), P(da.ptr), C.c_size_t(n * 4))
+    ms, _ = _time_loop(call, steps, warmup)
+    return {"ms": ms, "bytes": 8.0 * n}
+
+
 def wl_softmax(steps, warmup):
     rows, cols = 262144, 1024
     base = D.normal(D.SEED_ELT + 2, (1 << 24,))
@@ -266,7 +277,8 @@ def main() -> int:
     ap.add_argument("--no-suite", action="store_true", help="headline GEMM only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--workload", default="gemm4096",
-                    choices=["gemm4096", "mlp", "conv2d", "cnn", "eltwise", "softmax", "skinny"])
+                    choices=["gemm4096", "mlp", "conv2d", "cnn", "eltwise", "softmax", "skinny",
+                             "copy"])
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -280,7 +292,7 @@ def main() -> int:
     if args.workload != "gemm4096":
         # single-workload mode (used for profiling one kernel at a time)
         fn = {"mlp": wl_mlp, "conv2d": wl_conv, "cnn": wl_cnn, "eltwise": wl_eltwise,
-              "softmax": wl_softmax, "skinny": wl_skinny}[args.workload]
+              "softmax": wl_softmax, "skinny": wl_skinny, "copy": wl_copy}[args.workload]
         res = fn(steps, warmup)
         keep = {k: v for k, v in res.items() if isinstance(v, (int, float, dict))}
         print(json.dumps({"workload": args.workload, **keep}))

@@ -35,7 +35,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", f"-I{INCLUDE}",
 ]
-CXX_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wextra", "-Wno-unused-parameter",
+CXX_FLAGS = ["-O3", "-fPIC", "-std=c++20", "-Wall", "-Wextra", "-Wno-unused-parameter",
              "-ffp-contract=off", f"-I{INCLUDE}", f"-I{MOD_SRC}"]
 
 

@@ -5,9 +5,10 @@
 // into one pass, op for op:
 //   m  = first strict-'>' row max (tensorMaxAxis, runtime.cpp:924-963)
 //   mb = fl32(0.0 + m*1.0)         (reshape(m) @ ones([1,k]) broadcast)
-//   e  = fl32(exp(double(fl32(x - mb))))   (subtract, tensorExp 1013-1026)
+//   e  = fl32(exp(fl32(x - mb)))   (subtract, tensorExp 1013-1026; fp32 expf
+//                                   here, within 1 ulp of the fp64 libm exp)
 //   s  = fl32(sum_j double(e_j))   (tensorSumAxis 887-922, fp64 accumulation)
-//   y  = fl32(e / s)               (divide, "Division by zero" if s == 0)
+//   y  = fl32(e / s)               (divide, bit-exact through 1/s in fp64)
 // One wave owns one row; rows up to 64*4*ITEMS columns stay in registers, so
 // HBM sees one read and one write per element (8 B/elem).  The fp64 sum
 // differs from the reference's sequential order only in the last bits of
@@ -26,31 +27,6 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
-constexpr int NO_INDEX = 0x7fffffff;
-
-struct Best {
-    float v;
-    int i;
-};
-
-// b wins over a if it is a real candidate and larger, or equal and earlier.
-__device__ __forceinline__ Best best_of(Best a, Best b) {
-    if (b.i == NO_INDEX) return a;
-    if (a.i == NO_INDEX) return b;
-    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
-    return a;
-}
-
-__device__ __forceinline__ Best wave_best(Best b) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        Best o;
-        o.v = __shfl_xor(b.v, off);
-        o.i = __shfl_xor(b.i, off);
-        b = best_of(b, o);
-    }
-    return b;
-}
 
 __device__ __forceinline__ double wave_sum(double s) {
 #pragma unroll
@@ -58,20 +34,40 @@ __device__ __forceinline__ double wave_sum(double s) {
     return s;
 }
 
-// Candidate for a value at column index `idx`: NaN is skipped (a NaN never
-// compares greater); element 0 is handled by the caller.
-__device__ __forceinline__ Best candidate(float v, int idx) {
-    Best b;
-    b.v = v;
-    b.i = (v == v) ? idx : NO_INDEX;
-    return b;
+// Row max with the reference's rule (first element, then strict '>'), value
+// only: NaNs never win unless the row starts with one.  Which of several
+// equal maxima wins cannot change the softmax (m is only used as m + 0.0,
+// which also maps -0.0 to +0.0), so no index is tracked.
+__device__ __forceinline__ float max_gt(float best, float v) { return v > best ? v : best; }
+
+__device__ __forceinline__ float wave_max_gt(float m) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max_gt(m, __shfl_xor(m, off));
+    return m;
 }
 
-// ITEMS float4 per lane (VEC) or ITEMS*4 scalars per lane (!VEC).
+// e = exp(x - mb) rounded to fp32.  The device expf is within 1 ulp of the
+// reference's (float)std::exp((double)d); the softmax bar is rel-err 1e-6
+// (about 16 ulp), and fp32 exp keeps the kernel at HBM speed where the fp64
+// exp made it ALU-bound.
+__device__ __forceinline__ float softmax_exp(float v, float mb) { return expf(v - mb); }
+
+// y = fl32(e / s) bit-exactly, computed as fl32(e * fl64(1 / s)): the relative
+// error of the double product is <= 2^-52, while a quotient of two fp32 values
+// is never closer than 2^-49 (relative) to an fp32 rounding midpoint, so both
+// round to the same fp32 value.  This replaces a per-element fp32 division.
+__device__ __forceinline__ float softmax_div(float e, double rcp) {
+    return (float)((double)e * rcp);
+}
+
+// One wave per row, the whole row in registers: ITEMS float4 per lane (VEC,
+// cols % 4 == 0 and 16-byte aligned rows) or ITEMS*4 scalars per lane.  Slots
+// past the end of the row hold -inf, which never wins the max and adds an
+// exact 0 to the sum, so only the loads and stores are guarded.
 template <int ITEMS, bool VEC>
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restrict__ x,
                                                            float *__restrict__ y, int64_t rows,
-                                                           int cols, int *flag) {
+                                                           int cols) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -79,90 +75,81 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restri
     float *yr = y + row * cols;
     constexpr int NV = ITEMS * 4;
     float v[NV];
-    // Column of slot j (VEC: 4 consecutive columns per float4).
-    auto col_of = [&](int j) -> int {
-        return VEC ? 4 * (lane + WAVE * (j >> 2)) + (j & 3) : lane + WAVE * j;
-    };
     if constexpr (VEC) {
+        const int nq = cols >> 2;
 #pragma unroll
         for (int it = 0; it < ITEMS; ++it) {
-            const int c = 4 * (lane + WAVE * it);
-            f4 t = {0.f, 0.f, 0.f, 0.f};
-            if (c < cols) t = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr + c));
-            v[4 * it + 0] = t.x;
-            v[4 * it + 1] = t.y;
-            v[4 * it + 2] = t.z;
-            v[4 * it + 3] = t.w;
+            const int q = lane + WAVE * it;
+            f4 t = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            if (q < nq) t = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr) + q);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[4 * it + c] = t[c];
         }
     } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int c = col_of(j);
-            v[j] = c < cols ? xr[c] : 0.f;
+            const int c = lane + WAVE * j;
+            v[j] = c < cols ? xr[c] : -INFINITY;
         }
     }
-    Best b{0.f, NO_INDEX};
+    float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < NV; ++j)
-        if (col_of(j) < cols) b = best_of(b, candidate(v[j], col_of(j)));
-    b = wave_best(b);
-    const float x0 = __shfl(v[0], 0);
-    const float m = (x0 != x0) ? x0 : b.v;
-    const float mb = m + 0.0f; // fl32(0.0 + m * 1.0): -0.0 becomes +0.0
+    for (int j = 0; j < NV; ++j) m = max_gt(m, v[j]);
+    m = wave_max_gt(m);
+    const float x0 = __shfl(v[0], 0); // column 0 sits in lane 0, slot 0, in both layouts
+    if (x0 != x0) m = x0;
+    const float mb = m + 0.0f; // fl32(0.0 + m * 1.0): the ones-matmul broadcast
     double s = 0.0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        if (col_of(j) < cols) {
-            v[j] = (float)exp((double)(v[j] - mb));
-            s += (double)v[j];
-        }
+        v[j] = softmax_exp(v[j], mb);
+        s += (double)v[j];
     }
     s = wave_sum(s);
-    const float s32 = (float)s + 0.0f;
-    if (s32 == 0.0f && lane == 0) *flag = 1;
+    // s >= 1 (the max element contributes exp(0) = 1) or NaN, so the
+    // reference's "Division by zero" cannot occur here.
+    const double rcp = 1.0 / (double)(float)s;
     if constexpr (VEC) {
+        const int nq = cols >> 2;
 #pragma unroll
         for (int it = 0; it < ITEMS; ++it) {
-            const int c = 4 * (lane + WAVE * it);
-            if (c < cols) {
+            const int q = lane + WAVE * it;
+            if (q < nq) {
                 f4 t;
-                t.x = v[4 * it + 0] / s32;
-                t.y = v[4 * it + 1] / s32;
-                t.z = v[4 * it + 2] / s32;
-                t.w = v[4 * it + 3] / s32;
-                __builtin_nontemporal_store(t, reinterpret_cast<f4 *>(yr + c));
+#pragma unroll
+                for (int c = 0; c < 4; ++c) t[c] = softmax_div(v[4 * it + c], rcp);
+                __builtin_nontemporal_store(t, reinterpret_cast<f4 *>(yr) + q);
             }
         }
     } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int c = col_of(j);
-            if (c < cols) yr[c] = v[j] / s32;
+            const int c = lane + WAVE * j;
+            if (c < cols) yr[c] = softmax_div(v[j], rcp);
         }
     }
 }
 
-// Rows longer than the register budget: three passes over the row.
+// Rows longer than the register budget: max pass, sum pass, write pass.
 __global__ __launch_bounds__(256) void softmax_rows_long_kernel(const float *__restrict__ x,
                                                                 float *__restrict__ y,
-                                                                int64_t rows, int64_t cols,
-                                                                int *flag) {
+                                                                int64_t rows, int64_t cols) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float *xr = x + row * cols;
     float *yr = y + row * cols;
-    Best b{0.f, NO_INDEX};
-    for (int64_t c = lane; c < cols; c += WAVE) b = best_of(b, candidate(xr[c], (int)c));
-    b = wave_best(b);
+    float m = -INFINITY;
+    for (int64_t c = lane; c < cols; c += WAVE) m = max_gt(m, xr[c]);
+    m = wave_max_gt(m);
     const float x0 = xr[0];
-    const float mb = ((x0 != x0) ? x0 : b.v) + 0.0f;
+    if (x0 != x0) m = x0;
+    const float mb = m + 0.0f;
     double s = 0.0;
-    for (int64_t c = lane; c < cols; c += WAVE) s += (double)(float)exp((double)(xr[c] - mb));
+    for (int64_t c = lane; c < cols; c += WAVE) s += (double)softmax_exp(xr[c], mb);
     s = wave_sum(s);
-    const float s32 = (float)s + 0.0f;
-    if (s32 == 0.0f && lane == 0) *flag = 1;
-    for (int64_t c = lane; c < cols; c += WAVE) yr[c] = (float)exp((double)(xr[c] - mb)) / s32;
+    const double rcp = 1.0 / (double)(float)s;
+    for (int64_t c = lane; c < cols; c += WAVE) yr[c] = softmax_div(softmax_exp(xr[c], mb), rcp);
 }
 
 // axis = 1: one wave per row.  kind 0 = sum, 1 = max, 2 = argmax.
@@ -277,10 +264,10 @@ template <int ITEMS> int launch_softmax(const float *x, float *y, int64_t rows, 
     dim3 grid((unsigned)((rows + 3) / 4)), block(256);
     if (vec)
         hipLaunchKernelGGL((softmax_rows_kernel<ITEMS, true>), grid, block, 0, stream(), x, y, rows,
-                           cols, error_flag());
+                           cols);
     else
         hipLaunchKernelGGL((softmax_rows_kernel<ITEMS, false>), grid, block, 0, stream(), x, y,
-                           rows, cols, error_flag());
+                           rows, cols);
     return check_launch("softmax_rows_kernel");
 }
 
@@ -331,7 +318,6 @@ int camel_hip_softmax_rows(const float *x, float *y, int64_t rows, int64_t cols)
     if (cols > INT32_MAX / 2) return fail(CAMEL_HIP_ERR_SHAPE, "softmax: row too long");
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
-    CAMEL_RETURN_IF(clear_error_flag());
     const bool vec = (cols % 4 == 0) && (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
     const int c = (int)cols;
     if (cols <= 64 * 4)
@@ -342,14 +328,13 @@ int camel_hip_softmax_rows(const float *x, float *y, int64_t rows, int64_t cols)
         CAMEL_RETURN_IF(launch_softmax<4>(x, y, rows, c, vec));
     else if (cols <= 64 * 32)
         CAMEL_RETURN_IF(launch_softmax<8>(x, y, rows, c, vec));
+    else if (cols <= 64 * 64)
+        CAMEL_RETURN_IF(launch_softmax<16>(x, y, rows, c, vec));
     else {
         hipLaunchKernelGGL(softmax_rows_long_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                           stream(), x, y, rows, cols, error_flag());
+                           stream(), x, y, rows, cols);
         CAMEL_RETURN_IF(check_launch("softmax_rows_long_kernel"));
     }
-    int flag = 0;
-    CAMEL_RETURN_IF(read_error_flag(&flag));
-    if (flag) return fail(CAMEL_HIP_ERR_DIV_ZERO, "Division by zero");
     return ok();
 }
 

@@ -1,0 +1,156 @@
+// The slice of Camel's core runtime interface that the tensor operators are
+// written against, restated for this operator layer (libcamel_tensor.so).
+//
+// The operators keep the reference signature
+//     slot_t op(ArgsView &with, ArgsView &norm, Context &ctx)
+// (include/camel/core/operator.h:51-64) so that they can be registered by URI
+// suffix exactly like modules/tensor/operators.cpp:160-194.  The type codes
+// keep the reference's numeric values (include/camel/core/type/base.h:52-86)
+// and slots keep its bit layout (include/camel/core/rtdata/base.h:87-127):
+// pointers as integers, scalars smaller than 64 bits in the low bytes.
+#pragma once
+
+#include <cstdint>
+#include <cstring>
+#include <functional>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+namespace camel_amd {
+
+using slot_t = uint64_t;
+constexpr slot_t NullSlot = 0;
+
+// include/camel/core/type/base.h:52-67
+enum class TypeFlag : uint32_t {
+    Primitive = 0,
+    OtherType = 1u << 31,
+    Composite = 1u << 30,
+    GC_Traced = 1u << 29,
+    Auxiliary = 1u << 28,
+};
+constexpr uint32_t makeTypeCode(uint32_t flags, uint32_t id) { return flags | (id & 0x0FFFFFFF); }
+
+// include/camel/core/type/base.h:69-86 (same numeric codes).
+enum class TypeCode : uint32_t {
+    Int32 = makeTypeCode(0, 0x000),
+    Int64 = makeTypeCode(0, 0x001),
+    Float32 = makeTypeCode(0, 0x002),
+    Float64 = makeTypeCode(0, 0x003),
+    Bool = makeTypeCode(0, 0x004),
+    Byte = makeTypeCode(0, 0x005),
+    Void = makeTypeCode(0, 0x006),
+    String = makeTypeCode((uint32_t)TypeFlag::GC_Traced, 0x007),
+    Array = makeTypeCode((uint32_t)TypeFlag::Composite | (uint32_t)TypeFlag::GC_Traced, 0x008),
+    // The reference registers "Tensor" as an OtherType at run time
+    // (modules/tensor/type.cpp:38-40); this layer fixes its id to 1.
+    Tensor = makeTypeCode((uint32_t)TypeFlag::OtherType | (uint32_t)TypeFlag::Composite |
+                              (uint32_t)TypeFlag::GC_Traced,
+                          0x001),
+};
+
+// rtdata::toSlot / fromSlot (include/camel/core/rtdata/base.h:87-127).
+template <typename T> inline slot_t toSlot(const T &value) {
+    static_assert(sizeof(T) <= sizeof(slot_t) && std::is_trivially_copyable_v<T>);
+    if constexpr (std::is_pointer_v<T>) {
+        return static_cast<slot_t>(reinterpret_cast<std::uintptr_t>(value));
+    } else {
+        slot_t tmp = 0;
+        std::memcpy(&tmp, &value, sizeof(T));
+        return tmp;
+    }
+}
+template <typename T> inline T fromSlot(slot_t slot) {
+    static_assert(sizeof(T) <= sizeof(slot_t) && std::is_trivially_copyable_v<T>);
+    if constexpr (std::is_pointer_v<T>) {
+        return reinterpret_cast<T>(static_cast<std::uintptr_t>(slot));
+    } else {
+        T tmp;
+        std::memcpy(&tmp, &slot, sizeof(T));
+        return tmp;
+    }
+}
+
+// The error every tensor operator raises; the reference wraps
+// std::exception into RuntimeFault(RuntimeError, what()) with the same text
+// (modules/tensor/operators.cpp:103-109).
+class RuntimeFault : public std::runtime_error {
+  public:
+    explicit RuntimeFault(const std::string &msg) : std::runtime_error(msg) {}
+};
+[[noreturn]] inline void throwRuntimeFault(const std::string &msg) { throw RuntimeFault(msg); }
+
+// Camel Array value (rtdata Array): a typed sequence of slots.  Nested arrays
+// have elem == Array and hold ArrayObject pointers.
+struct ArrayObject {
+    TypeCode elem;
+    std::vector<slot_t> items;
+    size_t size() const { return items.size(); }
+};
+
+// include/camel/core/operator.h:51-62
+class ArgsView {
+  public:
+    virtual ~ArgsView() = default;
+    virtual size_t size() const = 0;
+    virtual slot_t slot(size_t index) const = 0;
+    virtual void setSlot(size_t index, slot_t value) = 0;
+    virtual TypeCode code(size_t index) const = 0;
+
+    template <typename T> T get(size_t index) const { return fromSlot<T>(slot(index)); }
+    template <typename T> void set(size_t index, T value) { setSlot(index, toSlot(value)); }
+};
+
+// A plain vector-backed view (the host harness's stand-in for FrameArgsView /
+// SlotArgsView, include/camel/core/context/frame.h:459-520).
+class VectorArgsView final : public ArgsView {
+  public:
+    VectorArgsView() = default;
+    VectorArgsView(std::vector<TypeCode> codes, std::vector<slot_t> slots)
+        : codes_(std::move(codes)), slots_(std::move(slots)) {}
+    void push(TypeCode code, slot_t slot) {
+        codes_.push_back(code);
+        slots_.push_back(slot);
+    }
+    size_t size() const override { return slots_.size(); }
+    slot_t slot(size_t index) const override { return slots_.at(index); }
+    void setSlot(size_t index, slot_t value) override { slots_.at(index) = value; }
+    TypeCode code(size_t index) const override { return codes_.at(index); }
+
+  private:
+    std::vector<TypeCode> codes_;
+    std::vector<slot_t> slots_;
+};
+
+// The execution context handed to every operator (unused by the tensor
+// operators, as in the reference).
+class Context {};
+
+using operator_t = slot_t (*)(ArgsView &with, ArgsView &norm, Context &ctx);
+
+// OperatorGroup: a name and its overloads, tried in order; the first resolver
+// that accepts the argument type codes wins (include/camel/core/operator.h:
+// 87-110, 297-307).  The resolver returns the result type code.
+using resolver_t = std::function<std::optional<TypeCode>(const std::vector<TypeCode> &with,
+                                                         const std::vector<TypeCode> &norm)>;
+struct OperatorGroup {
+    std::string name;
+    std::vector<std::pair<std::string, resolver_t>> overloads; // {uri, resolver}
+
+    // Returns the URI of the first matching overload and its result type.
+    std::optional<std::pair<std::string, TypeCode>>
+    resolve(const std::vector<TypeCode> &with, const std::vector<TypeCode> &norm) const {
+        for (const auto &[uri, fn] : overloads) {
+            if (auto t = fn(with, norm)) return std::make_pair(uri, *t);
+        }
+        return std::nullopt;
+    }
+};
+
+} // namespace camel_amd

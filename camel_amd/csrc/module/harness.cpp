@@ -1,0 +1,294 @@
+// Host harness of the operator layer: the extern "C" entry points of
+// include/camel_tensor.h.  It builds ArgsViews from {code, slot} pairs and
+// calls the registered operator_t exactly as the reference's executors do
+// (modules/tensor/executor.cpp:36-56: look the URI suffix up in the ops map,
+// call op(with, norm, ctx), store the result slot).
+#include "camel_tensor.h"
+
+#include "operators.h"
+#include "runtime.h"
+
+#include <algorithm>
+#include <mutex>
+#include <sstream>
+
+using namespace camel_amd;
+using namespace camel_amd::tensor;
+
+namespace {
+
+thread_local std::string t_error;
+
+int fail(int status, std::string msg) {
+    t_error = std::move(msg);
+    return status;
+}
+
+int ok() {
+    t_error.clear();
+    return CAMEL_TENSOR_OK;
+}
+
+const std::unordered_map<std::string, operator_t> &opsMap() {
+    static const auto map = getTensorOpsMap();
+    return map;
+}
+
+const std::vector<std::string> &opNames() {
+    static const std::vector<std::string> names = [] {
+        std::vector<std::string> v;
+        for (const auto &kv : opsMap()) v.push_back(kv.first);
+        std::sort(v.begin(), v.end());
+        return v;
+    }();
+    return names;
+}
+
+TensorObject *tensorOf(uint64_t handle) {
+    auto *t = fromSlot<TensorObject *>(handle);
+    return t && isLiveTensor(t) ? t : nullptr;
+}
+
+ArrayObject *arrayOf(uint64_t handle) {
+    auto *a = fromSlot<ArrayObject *>(handle);
+    return a && isLiveArray(a) ? a : nullptr;
+}
+
+// Builds a view over caller values, checking every handle is a live object
+// of the kind its code names.
+bool buildView(int64_t n, const camel_value *values, VectorArgsView &view, std::string &err) {
+    for (int64_t i = 0; i < n; ++i) {
+        const TypeCode code = static_cast<TypeCode>(values[i].code);
+        if (code == TypeCode::Tensor && values[i].slot != 0 && !tensorOf(values[i].slot)) {
+            err = "argument " + std::to_string(i) + " is not a live tensor handle";
+            return false;
+        }
+        if (code == TypeCode::Array && values[i].slot != 0 && !arrayOf(values[i].slot)) {
+            err = "argument " + std::to_string(i) + " is not a live array handle";
+            return false;
+        }
+        view.push(code, values[i].slot);
+    }
+    return true;
+}
+
+template <typename Fn> int guarded(Fn &&fn) {
+    try {
+        return fn();
+    } catch (const RuntimeFault &e) {
+        return fail(CAMEL_TENSOR_ERR_RUNTIME, e.what());
+    } catch (const std::exception &e) {
+        return fail(CAMEL_TENSOR_ERR_RUNTIME, e.what());
+    }
+}
+
+} // namespace
+
+extern "C" {
+
+const char *camel_tensor_last_error(void) { return t_error.c_str(); }
+
+int camel_tensor_abi_version(void) { return 1; }
+
+int camel_tensor_from_host(uint32_t dtype, int64_t rank, const int64_t *shape, const void *data,
+                           uint64_t *handle) {
+    if (!handle || rank < 0 || (rank > 0 && !shape))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_from_host: bad arguments");
+    return guarded([&] {
+        TensorObject *t = TensorObject::create(static_cast<TypeCode>(dtype),
+                                               std::span<const int64_t>(shape, (size_t)rank),
+                                               Residence::Host);
+        if (t->byteSize() > 0) {
+            if (!data) {
+                releaseTensor(t);
+                return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_from_host: null data");
+            }
+            std::memcpy(t->hostOutput(), data, t->byteSize());
+        }
+        *handle = toSlot(t);
+        return ok();
+    });
+}
+
+int camel_tensor_to_host(uint64_t handle, void *dst, size_t bytes) {
+    TensorObject *t = tensorOf(handle);
+    if (!t) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_to_host: not a live tensor");
+    if (bytes != t->byteSize() || (bytes > 0 && !dst))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_to_host: size mismatch");
+    return guarded([&] {
+        if (bytes > 0) std::memcpy(dst, t->hostData(), bytes);
+        return ok();
+    });
+}
+
+int camel_tensor_meta(uint64_t handle, uint32_t *dtype, int64_t *rank, int64_t *shape, int64_t cap) {
+    TensorObject *t = tensorOf(handle);
+    if (!t) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_meta: not a live tensor");
+    if (dtype) *dtype = static_cast<uint32_t>(t->dtype());
+    if (rank) *rank = (int64_t)t->rank();
+    for (int64_t i = 0; shape && i < cap && i < (int64_t)t->rank(); ++i) shape[i] = t->dim(i);
+    return ok();
+}
+
+int camel_tensor_residency(uint64_t handle, int *host_valid, int *device_valid) {
+    TensorObject *t = tensorOf(handle);
+    if (!t) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_residency: not a live tensor");
+    if (host_valid) *host_valid = t->hostValid() ? 1 : 0;
+    if (device_valid) *device_valid = t->deviceValid() ? 1 : 0;
+    return ok();
+}
+
+int camel_tensor_device_ptr(uint64_t handle, uint64_t *device_ptr) {
+    TensorObject *t = tensorOf(handle);
+    if (!t || !device_ptr) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_device_ptr: bad arguments");
+    return guarded([&] {
+        *device_ptr = toSlot(t->deviceData());
+        return ok();
+    });
+}
+
+int camel_tensor_release(uint64_t handle) {
+    auto *t = fromSlot<TensorObject *>(handle);
+    if (!t || !releaseTensor(t)) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_release: not a live tensor");
+    return ok();
+}
+
+int64_t camel_tensor_live_count(void) { return (int64_t)liveTensorCount(); }
+
+int64_t camel_tensor_release_all(void) { return (int64_t)releaseAll(); }
+
+int camel_tensor_format(uint64_t handle, char *buf, size_t cap, size_t *needed) {
+    TensorObject *t = tensorOf(handle);
+    if (!t) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_format: not a live tensor");
+    return guarded([&] {
+        std::ostringstream os;
+        t->print(os);
+        const std::string s = os.str();
+        if (needed) *needed = s.size() + 1;
+        if (buf && cap > 0) {
+            const size_t n = std::min(cap - 1, s.size());
+            std::memcpy(buf, s.data(), n);
+            buf[n] = '\0';
+        }
+        return ok();
+    });
+}
+
+int camel_tensor_equals(uint64_t a, uint64_t b, int *equal) {
+    TensorObject *ta = tensorOf(a), *tb = tensorOf(b);
+    if (!ta || !tb || !equal) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_equals: bad arguments");
+    return guarded([&] {
+        *equal = ta->equals(tb) ? 1 : 0;
+        return ok();
+    });
+}
+
+int camel_array_create(uint32_t elem_code, int64_t count, const uint64_t *slots, uint64_t *handle) {
+    if (!handle || count < 0 || (count > 0 && !slots))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_array_create: bad arguments");
+    const TypeCode elem = static_cast<TypeCode>(elem_code);
+    for (int64_t i = 0; elem == TypeCode::Array && i < count; ++i)
+        if (!arrayOf(slots[i])) return fail(CAMEL_TENSOR_ERR_ARG, "camel_array_create: bad nested array");
+    auto *a = new ArrayObject{elem, std::vector<slot_t>(slots, slots + count)};
+    registerObject(a);
+    *handle = toSlot(a);
+    return ok();
+}
+
+int camel_array_read(uint64_t handle, uint32_t *elem_code, int64_t *count, uint64_t *slots,
+                     int64_t cap) {
+    ArrayObject *a = arrayOf(handle);
+    if (!a) return fail(CAMEL_TENSOR_ERR_ARG, "camel_array_read: not a live array");
+    if (elem_code) *elem_code = static_cast<uint32_t>(a->elem);
+    if (count) *count = (int64_t)a->size();
+    for (int64_t i = 0; slots && i < cap && i < (int64_t)a->size(); ++i) slots[i] = a->items[i];
+    return ok();
+}
+
+int camel_array_release(uint64_t handle) {
+    auto *a = fromSlot<ArrayObject *>(handle);
+    if (!a || !releaseArray(a)) return fail(CAMEL_TENSOR_ERR_ARG, "camel_array_release: not a live array");
+    return ok();
+}
+
+int camel_tensor_invoke(const char *uri, int64_t n_with, const camel_value *with, int64_t n_norm,
+                        const camel_value *norm, camel_value *result) {
+    if (!uri || !result || n_with < 0 || n_norm < 0 || (n_with > 0 && !with) || (n_norm > 0 && !norm))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_invoke: bad arguments");
+    std::string key(uri);
+    if (key.rfind("tensor:", 0) == 0) key = key.substr(7);
+    auto it = opsMap().find(key);
+    if (it == opsMap().end()) return fail(CAMEL_TENSOR_ERR_URI, "Unrecognized operator URI: " + std::string(uri));
+    VectorArgsView withView, normView;
+    std::string err;
+    if (!buildView(n_with, with, withView, err) || !buildView(n_norm, norm, normView, err))
+        return fail(CAMEL_TENSOR_ERR_ARG, err);
+    // The result type is the one the operator's group resolves for these
+    // argument codes (the compiler fixes it in the reference).
+    std::vector<TypeCode> wc, nc;
+    for (int64_t i = 0; i < n_with; ++i) wc.push_back(static_cast<TypeCode>(with[i].code));
+    for (int64_t i = 0; i < n_norm; ++i) nc.push_back(static_cast<TypeCode>(norm[i].code));
+    std::optional<TypeCode> rtype;
+    const std::string full = "tensor:" + key;
+    for (const auto &g : getTensorOperatorGroups()) {
+        for (const auto &[guri, fn] : g.overloads) {
+            if (guri != full) continue;
+            if (auto t = fn(wc, nc)) rtype = t;
+            if (rtype) break;
+        }
+        if (rtype) break;
+    }
+    if (!rtype)
+        return fail(CAMEL_TENSOR_ERR_RESOLVE, "no overload of " + full + " accepts these argument types");
+    return guarded([&] {
+        Context ctx;
+        const slot_t out = it->second(withView, normView, ctx);
+        result->code = static_cast<uint32_t>(*rtype);
+        result->slot = out;
+        return ok();
+    });
+}
+
+int camel_tensor_resolve(const char *group, int64_t n_with, const uint32_t *with_codes,
+                         int64_t n_norm, const uint32_t *norm_codes, char *uri, size_t cap,
+                         uint32_t *result_code) {
+    if (!group || n_with < 0 || n_norm < 0 || (n_with > 0 && !with_codes) ||
+        (n_norm > 0 && !norm_codes))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_resolve: bad arguments");
+    std::vector<TypeCode> wc, nc;
+    for (int64_t i = 0; i < n_with; ++i) wc.push_back(static_cast<TypeCode>(with_codes[i]));
+    for (int64_t i = 0; i < n_norm; ++i) nc.push_back(static_cast<TypeCode>(norm_codes[i]));
+    bool found = false;
+    for (const auto &g : getTensorOperatorGroups()) {
+        if (g.name != group) continue;
+        found = true;
+        if (auto r = g.resolve(wc, nc)) {
+            if (uri && cap > 0) {
+                const size_t n = std::min(cap - 1, r->first.size());
+                std::memcpy(uri, r->first.data(), n);
+                uri[n] = '\0';
+            }
+            if (result_code) *result_code = static_cast<uint32_t>(r->second);
+            return ok();
+        }
+    }
+    if (!found) return fail(CAMEL_TENSOR_ERR_URI, "Unknown operator group: " + std::string(group));
+    return fail(CAMEL_TENSOR_ERR_RESOLVE, "no overload of " + std::string(group) + " accepts these argument types");
+}
+
+int64_t camel_tensor_op_count(void) { return (int64_t)opNames().size(); }
+
+const char *camel_tensor_op_name(int64_t index) {
+    if (index < 0 || index >= (int64_t)opNames().size()) return nullptr;
+    return opNames()[(size_t)index].c_str();
+}
+
+int64_t camel_tensor_group_count(void) { return (int64_t)getTensorOperatorGroups().size(); }
+
+const char *camel_tensor_group_name(int64_t index) {
+    const auto &g = getTensorOperatorGroups();
+    if (index < 0 || index >= (int64_t)g.size()) return nullptr;
+    return g[(size_t)index].name.c_str();
+}
+
+} // extern "C"

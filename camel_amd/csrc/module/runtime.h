@@ -1,0 +1,57 @@
+// Tensor kernels of the operator layer: the functions of the reference's
+// modules/tensor/runtime.h:116-165, same names and checks, running on the
+// gfx950 device through libcamel_hip (include/camel_hip.h), plus the layers
+// the reference composes in Camel source (relu, softmax, dense, conv2d,
+// maxpool2d).
+#pragma once
+
+#include "tensor_object.h"
+
+namespace camel_amd::tensor {
+
+TensorObject *tensorEmpty(TypeCode dtype, std::span<const int64_t> shape);
+TensorObject *tensorZeros(TypeCode dtype, std::span<const int64_t> shape);
+TensorObject *tensorOnes(TypeCode dtype, std::span<const int64_t> shape);
+TensorObject *tensorFull(TypeCode dtype, std::span<const int64_t> shape, double value);
+TensorObject *tensorRandom(std::span<const int64_t> shape, double low, double high);
+TensorObject *tensorArange(int64_t start, int64_t stop, int64_t step);
+TensorObject *tensorEye(int64_t size);
+TensorObject *tensorReshape(const TensorObject *tensor, std::span<const int64_t> shape);
+TensorObject *tensorTranspose2D(const TensorObject *tensor);
+TensorObject *tensorConcat(const TensorObject *lhs, const TensorObject *rhs, int64_t axis);
+TensorObject *tensorBinary(const TensorObject *lhs, const TensorObject *rhs, BinaryOp op);
+TensorObject *tensorBinaryScalarRight(const TensorObject *lhs, TypeCode rhsType, slot_t rhs,
+                                      BinaryOp op);
+TensorObject *tensorBinaryScalarLeft(TypeCode lhsType, slot_t lhs, const TensorObject *rhs,
+                                     BinaryOp op);
+TensorObject *tensorCompareScalarRight(const TensorObject *lhs, TypeCode rhsType, slot_t rhs,
+                                       CompareOp op);
+TensorObject *tensorCompareScalarLeft(TypeCode lhsType, slot_t lhs, const TensorObject *rhs,
+                                      CompareOp op);
+TensorObject *tensorCompare(const TensorObject *lhs, const TensorObject *rhs, CompareOp op);
+TensorObject *tensorMatmul(const TensorObject *lhs, const TensorObject *rhs);
+
+double tensorSum(const TensorObject *tensor);
+TensorObject *tensorSumAxis(const TensorObject *tensor, int64_t axis);
+TensorObject *tensorMaxAxis(const TensorObject *tensor, int64_t axis);
+TensorObject *tensorArgmaxAxis(const TensorObject *tensor, int64_t axis);
+TensorObject *tensorExp(const TensorObject *tensor);
+TensorObject *tensorLog(const TensorObject *tensor);
+double tensorIndex1D(const TensorObject *tensor, int64_t index);
+double tensorIndex2D(const TensorObject *tensor, int64_t row, int64_t col);
+
+// Layers with no reference operator, defined by the reference compositions:
+// relu(x) = x * (x > 0) (test/run/nn/svm.cml:31); softmax = the row softmax of
+// test/run/nn/mnist.cml:13-25; dense = x @ W (+ ones @ b) (mnist.cml:18,
+// README.md:40-46), optionally followed by relu; conv2d = direct NCHW
+// convolution with matmul semantics, optional bias and relu; maxpool2d =
+// window max with tensorMaxAxis's first-strict-'>' rule.
+TensorObject *tensorRelu(const TensorObject *tensor);
+TensorObject *tensorSoftmax(const TensorObject *tensor);
+TensorObject *tensorDense(const TensorObject *x, const TensorObject *w, const TensorObject *bias,
+                          bool relu);
+TensorObject *tensorConv2d(const TensorObject *x, const TensorObject *w, const TensorObject *bias,
+                           int64_t stride, int64_t pad, bool relu);
+TensorObject *tensorMaxPool2d(const TensorObject *x, int64_t kernel, int64_t stride);
+
+} // namespace camel_amd::tensor

@@ -1,0 +1,146 @@
+// TensorObject with device residency: the Tensor value of the reference's
+// tensor module (modules/tensor/runtime.h:55-109) re-laid out for a GPU.
+//
+// The reference keeps the payload inline behind the header in GC memory
+// (runtime.cpp:256-279, 482-485).  Here the header keeps the same fields
+// (dtype, rank, numel, byteSize, shape) and the payload lives in a Storage
+// block that has a device copy (HBM, from libcamel_hip's pool) and/or a host
+// copy.  Tensors are immutable once an operator has produced them (the
+// reference's operators never mutate their inputs), so the two copies are
+// kept coherent by validity flags alone:
+//   * operator outputs are born on the device (dev_valid only);
+//   * tensors built from host data are born on the host and uploaded at the
+//     first device use (then both are valid);
+//   * host reads (index, print, equals, to_host) download once and cache.
+// reshape returns a view that shares the Storage (the reference copies; the
+// values are the same because neither copy is ever written again).
+#pragma once
+
+#include "camel_core.h"
+
+#include <cstddef>
+#include <iosfwd>
+#include <memory>
+#include <mutex>
+#include <span>
+#include <vector>
+
+namespace camel_amd::tensor {
+
+// modules/tensor/runtime.h:39-53
+enum class BinaryOp { Add, Subtract, Multiply, Divide, Power };
+enum class CompareOp { Less, LessEqual, Greater, GreaterEqual, Equal };
+
+// Where a new tensor's payload is first materialised.
+enum class Residence { Device, Host };
+
+// Throws RuntimeFault with the shim's message when a libcamel_hip call fails.
+void checkHip(int status);
+
+struct Storage {
+    explicit Storage(size_t bytes) : bytes(bytes) {}
+    ~Storage();
+    Storage(const Storage &) = delete;
+    Storage &operator=(const Storage &) = delete;
+
+    size_t bytes;
+    void *dev = nullptr;
+    std::unique_ptr<std::byte[]> host;
+    bool devValid = false;
+    bool hostValid = false;
+    std::mutex mutex; // residency transitions may race under a thread-pool scheduler
+};
+
+class TensorObject {
+  public:
+    TensorObject(const TensorObject &) = delete;
+    TensorObject &operator=(const TensorObject &) = delete;
+
+    // TensorObject::create (runtime.cpp:256-279).  dtype is normalised
+    // (Float64 -> Float32, Int32 -> Int64).  zeroInit fills with zeros.
+    static TensorObject *create(TypeCode dtype, std::span<const int64_t> shape, Residence where,
+                                bool zeroInit = false);
+    // A tensor of `shape` sharing `src`'s payload (numel must match).
+    static TensorObject *view(const TensorObject *src, std::span<const int64_t> shape);
+
+    size_t rank() const { return shape_.size(); }
+    uint64_t numel() const { return numel_; }
+    TypeCode dtype() const { return dtype_; }
+    size_t byteSize() const { return byteSize_; }
+    const int64_t *shape() const { return shape_.data(); }
+    int64_t dim(size_t index) const;
+    bool sameShape(const TensorObject *other) const;
+
+    // Device pointer of a valid device copy (uploads a host-only payload).
+    const void *deviceData() const;
+    // Device pointer for an operator that fills the payload on the device:
+    // the device copy becomes the only valid one.
+    void *deviceOutput();
+    // Host pointer of a valid host copy (downloads a device-only payload).
+    const void *hostData() const;
+    // Host pointer for a writer that fills the payload on the host.
+    void *hostOutput();
+
+    bool hostValid() const;
+    bool deviceValid() const;
+
+    // Element access with the reference's conversions (runtime.cpp:298-389).
+    // A device-only tensor is not downloaded whole: one element is copied.
+    double getAsDouble(uint64_t flatIndex) const;
+    int64_t getAsInt64(uint64_t flatIndex) const;
+    bool getAsBool(uint64_t flatIndex) const;
+
+    // rtdata::Object behaviour (runtime.cpp:391-420, 422-500).
+    bool equals(const TensorObject *other) const;
+    TensorObject *clone() const;
+    void print(std::ostream &os) const;
+
+  private:
+    TensorObject(TypeCode dtype, std::vector<int64_t> shape, uint64_t numel, size_t byteSize,
+                 std::shared_ptr<Storage> storage)
+        : dtype_(dtype), shape_(std::move(shape)), numel_(numel), byteSize_(byteSize),
+          storage_(std::move(storage)) {}
+    void readElement(uint64_t flatIndex, void *dst) const;
+    void printRecursive(std::ostream &os, size_t dimIndex, uint64_t &flatIndex,
+                        const std::string &indent, const std::byte *data) const;
+    std::string formatElement(const std::byte *data, uint64_t flatIndex) const;
+
+    TypeCode dtype_;
+    std::vector<int64_t> shape_;
+    uint64_t numel_;
+    size_t byteSize_;
+    std::shared_ptr<Storage> storage_;
+};
+
+// modules/tensor/runtime.cpp:530-580
+size_t elementSize(TypeCode dtype);
+bool isSupportedTensorScalar(TypeCode code);
+bool isFloatingTensorType(TypeCode code);
+TypeCode normalizeTensorDType(TypeCode code);
+TypeCode tensorDTypeFromValueType(TypeCode code);
+TypeCode promoteTensorTypes(TypeCode lhs, TypeCode rhs);
+// dtype code of libcamel_hip (CAMEL_DT_*) for a storage dtype.
+int hipDType(TypeCode dtype);
+
+// Scalar conversions of runtime.cpp:62-111.
+double scalarToDouble(TypeCode code, slot_t value);
+
+// Tensor <-> Array values (runtime.cpp:152-226, 582-612, 1067-1077).
+std::vector<int64_t> parseShapeArray(const ArrayObject *shapeArray, TypeCode shapeCode);
+ArrayObject *makeShapeArray(const TensorObject *tensor);
+TensorObject *tensorFromArray(slot_t slot, TypeCode valueCode);
+
+// Tensor-lifetime bookkeeping: every TensorObject / ArrayObject made by this
+// layer is registered so a host program (or a graph's end) can release it.
+// The reference never frees tensors (no finalizers, GC roots unset).
+void registerObject(TensorObject *t);
+void registerObject(ArrayObject *a);
+bool releaseTensor(TensorObject *t);
+bool releaseArray(ArrayObject *a);
+bool isLiveTensor(const TensorObject *t);
+bool isLiveArray(const ArrayObject *a);
+size_t liveTensorCount();
+// Releases every registered tensor and array; returns how many objects.
+size_t releaseAll();
+
+} // namespace camel_amd::tensor

@@ -1,0 +1,115 @@
+/*
+ * camel_tensor.h -- C-ABI of libcamel_tensor.so, the operator layer of the
+ * Camel `tensor` module on the MI355X backend.
+ *
+ * The layer keeps the reference's operator API: every operator of
+ * modules/tensor/operators.cpp:160-194 is registered under the same URI
+ * suffix ("matmul", "add", ...) with the same argument conventions, result
+ * types and error texts, and the layer operators relu / softmax / dense /
+ * dense_relu / conv2d / conv2d_relu / maxpool2d are added under "tensor:".
+ * This header is the host harness that drives those operators without the
+ * Camel runtime, the role FrameArgsView plays in the reference
+ * (include/camel/core/context/frame.h:459-492): values are {type code, slot}
+ * pairs with the reference's type codes (include/camel/core/type/base.h:69-86)
+ * and slot layout (include/camel/core/rtdata/base.h:87-127).
+ *
+ * Tensors are opaque handles.  Their payload lives on the GPU from the first
+ * device operator until a host read (to_host, idx, show, equals) brings a
+ * copy back; operators never copy through the host between each other.
+ * Handles are released explicitly (the reference never frees tensors).
+ * Status codes: 0 OK, otherwise an error whose text (the reference's
+ * RuntimeFault message, e.g. "matmul dimension mismatch") is returned by
+ * camel_tensor_last_error().
+ */
+#ifndef CAMEL_TENSOR_H
+#define CAMEL_TENSOR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum camel_tensor_status {
+    CAMEL_TENSOR_OK = 0,
+    CAMEL_TENSOR_ERR_RUNTIME = 1, /* RuntimeFault raised by an operator         */
+    CAMEL_TENSOR_ERR_URI = 2,     /* no operator / group with that name         */
+    CAMEL_TENSOR_ERR_ARG = 3,     /* bad handle, code or size at this interface */
+    CAMEL_TENSOR_ERR_RESOLVE = 4  /* no overload accepts the argument types     */
+};
+
+/* Type codes (same values as the reference's TypeCode). */
+#define CAMEL_TC_INT32 0x00000000u
+#define CAMEL_TC_INT64 0x00000001u
+#define CAMEL_TC_FLOAT32 0x00000002u
+#define CAMEL_TC_FLOAT64 0x00000003u
+#define CAMEL_TC_BOOL 0x00000004u
+#define CAMEL_TC_VOID 0x00000006u
+#define CAMEL_TC_ARRAY 0x60000008u
+/* "Tensor" is an OtherType the reference numbers at run time
+ * (modules/tensor/type.cpp:38-40); this layer fixes it here. */
+#define CAMEL_TC_TENSOR 0xE0000001u
+
+/* One operator argument or result. */
+typedef struct camel_value {
+    uint32_t code; /* CAMEL_TC_* */
+    uint64_t slot; /* scalar bits in the low bytes, or a handle */
+} camel_value;
+
+const char *camel_tensor_last_error(void);
+
+/* ---- tensors ------------------------------------------------------------- */
+/* A host tensor of dtype (FLOAT32 / INT64 / BOOL; FLOAT64 and INT32 are
+ * normalised as the reference does) copied from `data` (numel * element size
+ * bytes; may be NULL for numel == 0).  It is uploaded at its first device use. */
+int camel_tensor_from_host(uint32_t dtype, int64_t rank, const int64_t *shape, const void *data,
+                           uint64_t *handle);
+/* Copies the payload to `dst` (exactly byte_size bytes), downloading once. */
+int camel_tensor_to_host(uint64_t handle, void *dst, size_t bytes);
+/* dtype, rank and up to `cap` dims. */
+int camel_tensor_meta(uint64_t handle, uint32_t *dtype, int64_t *rank, int64_t *shape, int64_t cap);
+/* Where the payload is currently valid (1/0 each). */
+int camel_tensor_residency(uint64_t handle, int *host_valid, int *device_valid);
+/* Device address of the payload (uploading if needed), e.g. for DLPack/torch. */
+int camel_tensor_device_ptr(uint64_t handle, uint64_t *device_ptr);
+int camel_tensor_release(uint64_t handle);
+/* Releases every tensor and array this layer has made; returns how many. */
+int64_t camel_tensor_release_all(void);
+int64_t camel_tensor_live_count(void);
+/* Writes the reference print form (TensorObject::print) into buf. */
+int camel_tensor_format(uint64_t handle, char *buf, size_t cap, size_t *needed);
+/* TensorObject::equals: same dtype, shape and bytes. */
+int camel_tensor_equals(uint64_t a, uint64_t b, int *equal);
+
+/* ---- arrays (shape arguments, array operands, shape() results) ----------- */
+int camel_array_create(uint32_t elem_code, int64_t count, const uint64_t *slots, uint64_t *handle);
+int camel_array_read(uint64_t handle, uint32_t *elem_code, int64_t *count, uint64_t *slots,
+                     int64_t cap);
+int camel_array_release(uint64_t handle);
+
+/* ---- operators ----------------------------------------------------------- */
+/* Calls the operator registered under `uri` ("tensor:matmul" or "matmul")
+ * with bind arguments `with` and normal arguments `norm`; the result's type
+ * is the one the operator group resolves for these argument types. */
+int camel_tensor_invoke(const char *uri, int64_t n_with, const camel_value *with, int64_t n_norm,
+                        const camel_value *norm, camel_value *result);
+/* Overload resolution of a group ("__mat__", "sum", "dense", ...): writes the
+ * chosen URI and the result type code. */
+int camel_tensor_resolve(const char *group, int64_t n_with, const uint32_t *with_codes,
+                         int64_t n_norm, const uint32_t *norm_codes, char *uri, size_t cap,
+                         uint32_t *result_code);
+/* Registered URI suffixes and group names. */
+int64_t camel_tensor_op_count(void);
+const char *camel_tensor_op_name(int64_t index);
+int64_t camel_tensor_group_count(void);
+const char *camel_tensor_group_name(int64_t index);
+
+/* Plugin ABI version the reference's loader checks (dynamic.h:29). */
+int camel_tensor_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -5,6 +5,8 @@ concat, argmax, max (NaN payloads aside), axis-0 sums (same order as the
 reference); fp64-order-dependent results (axis-1 sums, whole sums, softmax)
 within rel-err 1e-6; libm calls (exp/log/pow) within rel-err 1e-6 and
 otherwise expected bit-equal (ocml vs glibc differ below fp32 rounding);
+softmax uses the fp32 device expf (within 1 ulp of fl32(exp(double))), so
+most but not all of its outputs are bit-equal, all within rel-err 1e-6;
 conv2d under the GEMM bound 1e-5*sqrt(K)*sum|x||w|.
 """
 import ctypes as C
@@ -196,8 +198,10 @@ def test_softmax_matches_composition(rows, cols):
     dx, dy = K.dev(x), K.empty(x.nbytes)
     H.call("camel_hip_softmax_rows", P(dx.ptr), P(dy.ptr), rows, cols)
     got, ref = K.host(dy, F, x.shape), O.softmax_rows(x)
+    # north-star softmax tolerance: rel-err <= 1e-6 per element
     assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-38)) <= 1e-6
-    assert np.mean(got == ref) > 0.999
+    assert np.mean(got == ref) > 0.75
+    np.testing.assert_allclose(got.sum(axis=1, dtype=np.float64), 1.0, rtol=2e-6)
 
 
 def test_softmax_nan_and_ties():
@@ -205,7 +209,11 @@ def test_softmax_nan_and_ties():
                   [5.0, 5.0, 5.0, 5.0]], F)
     dx, dy = K.dev(x), K.empty(x.nbytes)
     H.call("camel_hip_softmax_rows", P(dx.ptr), P(dy.ptr), 4, 4)
-    assert bits_equal(K.host(dy, F, x.shape), O.softmax_rows(x))
+    got, ref = K.host(dy, F, x.shape), O.softmax_rows(x)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.isnan(got[:2]).all()  # a NaN anywhere in a row poisons the fp64 row sum
+    np.testing.assert_allclose(got[2:], ref[2:], rtol=1e-6)
+    assert bits_equal(got[3], ref[3])  # ties: exp(0) = 1 exactly, 1/4 exactly
 
 
 # ----------------------------------------------------------- reductions

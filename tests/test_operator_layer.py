@@ -1,0 +1,238 @@
+"""CPU tests of the operator layer (libcamel_tensor.so) and of the C-ABI.
+
+Everything here runs without a GPU: the libraries load, export what the
+headers declare, the operator map and overload resolution mirror the
+reference's (modules/tensor/operators.cpp:160-583), and the argument and
+shape errors the reference raises before touching data are raised with the
+same text.  Host tensors stay on the host until a device operator needs them,
+so these error paths never reach libcamel_hip's device code.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from camel_amd import _hip as H
+from camel_amd import tensor as T
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+# modules/tensor/operators.cpp:160-194
+REFERENCE_OPS = {"add", "subtract", "multiply", "divide", "pow", "matmul", "idx", "idx2d", "lt",
+                 "le", "gt", "ge", "eq", "empty", "zeros", "ones", "full", "random", "range", "eye",
+                 "shape", "sum", "sum_axis", "max_axis", "argmax_axis", "exp", "log", "transpose",
+                 "concat", "reshape", "show"}
+LAYER_OPS = {"relu", "softmax", "dense", "dense_relu", "conv2d", "conv2d_relu", "maxpool2d"}
+
+
+def declared_functions(header: str) -> set[str]:
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(camel_\w+)\s*\(", text))
+
+
+@pytest.fixture(autouse=True)
+def _release():
+    yield
+    T.release_all()
+
+
+def test_hip_abi_exports_every_declared_symbol():
+    lib = H.load()
+    declared = declared_functions("camel_hip.h")
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared == set(H.exported_symbols())
+
+
+def test_tensor_abi_exports_every_declared_symbol():
+    lib = T.load()
+    declared = declared_functions("camel_tensor.h")
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared == set(T.exported_symbols())
+    assert lib.camel_tensor_abi_version() == 1
+
+
+def test_ops_map_keeps_reference_suffixes():
+    names = set(T.op_names())
+    assert REFERENCE_OPS <= names
+    assert names == REFERENCE_OPS | LAYER_OPS
+
+
+def test_groups_keep_reference_names():
+    groups = set(T.group_names())
+    for g in ["__add__", "__sub__", "__mul__", "__div__", "__pow__", "__mat__", "__idx__", "__lt__",
+              "__le__", "__gt__", "__ge__", "__eq__", "empty", "zeros", "ones", "full", "random",
+              "range", "eye", "shape", "sum", "max", "argmax", "exp", "log", "transpose", "concat",
+              "reshape", "show", "add", "subtract", "multiply", "divide", "pow", "matmul"]:
+        assert g in groups, g
+    assert LAYER_OPS <= groups
+
+
+@pytest.mark.parametrize("group,norm,with_,uri,result", [
+    ("__mat__", [T.TC_TENSOR, T.TC_TENSOR], [], "tensor:matmul", T.TC_TENSOR),
+    ("__add__", [T.TC_TENSOR, T.TC_FLOAT64], [], "tensor:add", T.TC_TENSOR),
+    ("__add__", [T.TC_INT32, T.TC_TENSOR], [], "tensor:add", T.TC_TENSOR),
+    ("__idx__", [T.TC_TENSOR, T.TC_INT64], [], "tensor:idx", T.TC_FLOAT64),
+    ("__idx__", [T.TC_TENSOR, T.TC_INT64, T.TC_INT64], [], "tensor:idx2d", T.TC_FLOAT64),
+    ("sum", [T.TC_TENSOR], [], "tensor:sum", T.TC_FLOAT64),
+    ("sum", [T.TC_TENSOR, T.TC_INT32], [], "tensor:sum_axis", T.TC_TENSOR),
+    ("__eq__", [T.TC_ARRAY, T.TC_FLOAT32], [], "tensor:eq", T.TC_TENSOR),
+    ("__lt__", [T.TC_ARRAY, T.TC_FLOAT64], [], "tensor:lt", T.TC_TENSOR),
+    ("range", [T.TC_INT64, T.TC_INT64, T.TC_INT32], [], "tensor:range", T.TC_TENSOR),
+    ("shape", [T.TC_TENSOR], [], "tensor:shape", T.TC_ARRAY),
+    ("show", [T.TC_ARRAY], [], "tensor:show", T.TC_VOID),
+    ("dense", [T.TC_TENSOR], [T.TC_TENSOR, T.TC_TENSOR], "tensor:dense", T.TC_TENSOR),
+    ("dense_relu", [T.TC_TENSOR, T.TC_TENSOR], [], "tensor:dense_relu", T.TC_TENSOR),
+    ("conv2d", [T.TC_TENSOR], [T.TC_TENSOR, T.TC_TENSOR, T.TC_INT64, T.TC_INT64], "tensor:conv2d",
+     T.TC_TENSOR),
+    ("maxpool2d", [T.TC_TENSOR], [T.TC_INT64], "tensor:maxpool2d", T.TC_TENSOR),
+])
+def test_resolution(group, norm, with_, uri, result):
+    assert T.resolve(group, norm, with_) == (uri, result)
+
+
+@pytest.mark.parametrize("group,norm", [
+    ("__mat__", [T.TC_TENSOR, T.TC_FLOAT64]),     # matmul takes two tensors only
+    ("__add__", [T.TC_FLOAT64, T.TC_FLOAT64]),    # no tensor operand
+    ("__pow__", [T.TC_FLOAT64, T.TC_TENSOR]),     # base must be a tensor
+    ("__lt__", [T.TC_ARRAY, T.TC_ARRAY]),         # two arrays: not a compare overload
+])
+def test_resolution_rejects(group, norm):
+    with pytest.raises(T.CamelError, match="no overload"):
+        T.resolve(group, norm)
+
+
+def host(a):
+    return T.Tensor.from_numpy(np.asarray(a))
+
+
+@pytest.mark.parametrize("uri,args,msg", [
+    ("add", lambda: (host(np.zeros((2, 3), np.float32)), host(np.zeros((3, 2), np.float32))),
+     "Tensor binary operation requires matching shapes"),
+    ("lt", lambda: (host(np.zeros(3, np.float32)), host(np.zeros(4, np.float32))),
+     "Tensor comparison requires matching shapes"),
+    ("matmul", lambda: (host(np.zeros(3, np.float32)), host(np.zeros((3, 2), np.float32))),
+     "matmul currently only supports rank-2 tensors"),
+    ("matmul", lambda: (host(np.zeros((2, 3), np.float32)), host(np.zeros((2, 2), np.float32))),
+     "matmul dimension mismatch"),
+    ("transpose", lambda: (host(np.zeros(3, np.float32)),),
+     "transpose currently only supports rank-2 tensors"),
+    ("concat", lambda: (host(np.zeros((2, 2), np.float32)), host(np.zeros(2, np.float32)), 0),
+     "concat requires tensors with the same rank"),
+    ("concat", lambda: (host(np.zeros((2, 2), np.float32)), host(np.zeros((2, 2), np.float32)), 2),
+     "concat axis out of range"),
+    ("concat", lambda: (host(np.zeros((2, 2), np.float32)), host(np.zeros((2, 2), np.int64)), 0),
+     "concat currently requires matching dtypes"),
+    ("concat", lambda: (host(np.zeros((2, 2), np.float32)), host(np.zeros((2, 3), np.float32)), 0),
+     "concat requires equal non-axis dimensions"),
+    ("reshape", lambda: (host(np.zeros((2, 3), np.float32)), [4, 2]),
+     "reshape changes tensor element count"),
+    ("reshape", lambda: (host(np.zeros((2, 3), np.float32)), [-1, 6]),
+     "Shape cannot contain negative values"),
+    ("reshape", lambda: (host(np.zeros((2, 3), np.float32)), [2.0, 3.0]),
+     "Shape array must contain integers"),
+    ("idx", lambda: (host(np.zeros((2, 2), np.float32)), 0),
+     "Single-index tensor access requires rank-1 tensor"),
+    ("idx", lambda: (host(np.zeros(3, np.float32)), 3), "Tensor index out of bounds"),
+    ("idx2d", lambda: (host(np.zeros((2, 2), np.float32)), 0, -1), "Tensor index out of bounds"),
+    ("range", lambda: (0, 5, 0), "range step cannot be zero"),
+    ("eye", lambda: (-1,), "eye size cannot be negative"),
+    ("sum_axis", lambda: (host(np.zeros(3, np.float32)), 0),
+     r"sum\(axis\) currently only supports rank-2 tensors"),
+    ("max_axis", lambda: (host(np.zeros((2, 2), np.float32)), 2),
+     r"max\(axis\): axis must be 0 or 1 for rank-2 tensors"),
+    ("argmax_axis", lambda: (host(np.zeros((2, 2), np.float32)), -3),
+     r"argmax\(axis\): axis must be 0 or 1 for rank-2 tensors"),
+    ("exp", lambda: (host(np.zeros(3, np.int64)),), "exp requires floating-point tensor"),
+    ("log", lambda: (host(np.zeros(3, np.uint8)),), "log requires floating-point tensor"),
+    ("eq", lambda: ([[1, 2], [3]], 1.0), "Nested array shape or dtype mismatch"),
+    ("softmax", lambda: (host(np.zeros(3, np.float32)),), "softmax currently only supports rank-2"),
+])
+def test_reference_errors_before_any_device_work(uri, args, msg):
+    with pytest.raises(T.CamelError, match=msg) as info:
+        T.call(uri, *args())
+    assert info.value.status == T.ERR_RUNTIME
+
+
+def test_dense_and_conv_argument_errors():
+    x = host(np.zeros((4, 3), np.float32))
+    w = host(np.zeros((2, 5), np.float32))
+    with pytest.raises(T.CamelError, match="dense dimension mismatch"):
+        T.call("dense", x, with_=(w,))
+    with pytest.raises(T.CamelError, match="no overload of tensor:dense") as info:
+        T.call("dense", x)  # the group's resolver wants weights
+    assert info.value.status == T.ERR_RESOLVE
+    x4 = host(np.zeros((1, 3, 4, 4), np.float32))
+    w4 = host(np.zeros((2, 2, 3, 3), np.float32))
+    with pytest.raises(T.CamelError, match="conv2d channel mismatch"):
+        T.call("conv2d", x4, with_=(w4,))
+    with pytest.raises(T.CamelError, match="maxpool2d window larger than input"):
+        T.call("maxpool2d", x4, with_=(5,))
+
+
+def test_ill_typed_calls_fail_resolution():
+    # As in the reference, the group's resolver decides which argument types
+    # reach an operator; anything else is rejected before the operator runs.
+    for uri, args in [("transpose", (1.0,)), ("matmul", (host(np.zeros((1, 1), np.float32)), 1.0)),
+                      ("range", (1.5,))]:
+        with pytest.raises(T.CamelError, match="no overload") as info:
+            T.call(uri, *args)
+        assert info.value.status == T.ERR_RESOLVE
+
+
+def test_unknown_uri_and_bad_handles():
+    with pytest.raises(T.CamelError, match="Unrecognized operator URI") as info:
+        T.call("tensor:conv3d", host(np.zeros(1, np.float32)))
+    assert info.value.status == T.ERR_URI
+    bogus = T.Tensor(0xDEAD0)
+    with pytest.raises(T.CamelError, match="not a live tensor"):
+        T.call("transpose", bogus)
+
+
+def test_host_only_values_need_no_device():
+    a = host(np.arange(6, dtype=np.float32).reshape(2, 3))
+    assert a.residency() == (True, False)
+    assert T.call("shape", a) == [2, 3]
+    assert T.call("idx2d", a, 1, 2) == 5.0
+    assert a.residency() == (True, False)
+    b = T.call("reshape", a, [3, 2])  # a view: shares the payload, no copy
+    assert b.shape == (3, 2)
+    assert np.array_equal(b.numpy(), np.arange(6, dtype=np.float32).reshape(3, 2))
+    assert b.residency() == (True, False)
+    assert a.equals(a) and not a.equals(b)
+
+
+def test_print_format_matches_reference():
+    # TensorObject::print (modules/tensor/runtime.cpp:422-528).
+    eye = host(np.eye(2, dtype=np.float32))
+    assert eye.format() == ("tensor([[      1.,       0.],\n"
+                            "        [      0.,       1.]], dtype=float32)")
+    assert host(np.array([1.5, -0.25], np.float32)).format() == \
+        "tensor([    1.5,   -0.25], dtype=float32)"
+    assert host(np.array([3, -4], np.int64)).format() == "tensor([      3,      -4], dtype=int64)"
+    assert host(np.array([1, 0], np.uint8)).format() == "tensor([  true,  false], dtype=bool)"
+    long_row = host(np.arange(20, dtype=np.int64)).format()
+    assert long_row.startswith("tensor([      0,") and ",\n        " in long_row
+
+
+def test_array_round_trip_and_tensor_from_nested_array():
+    arr = T.Array.from_list([[1, 2], [3, 4]])
+    assert arr.to_list() == [[1, 2], [3, 4]]
+    t = T.call("reshape", arr, [4])  # requireTensorOrConvertArray builds a host tensor
+    assert t.dtype_code == T.TC_INT64
+    assert t.numpy().tolist() == [1, 2, 3, 4]
+
+
+def test_release_bookkeeping():
+    T.release_all()
+    a = host(np.zeros(4, np.float32))
+    assert T.live_count() == 1
+    a.release()
+    assert T.live_count() == 0
+    with pytest.raises(T.CamelError):
+        a.handle = 12345
+        a.release()
