@@ -34,8 +34,12 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int GROUP_M = 4;
 
-// Operand loader kinds.
-enum { LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2 };
+// Operand loader kinds.  LOAD_CONV gathers im2col columns from NCHW x one
+// float at a time; LOAD_NHWC reads x in NHWC with K ordered (kh, kw, c), so
+// each k-quad of a pixel is one 16-byte load (needs C % BK == 0).
+enum { LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3 };
+
+template <int M> constexpr bool is_conv = (M == LOAD_CONV || M == LOAD_NHWC);
 
 template <int BM_, int BN_, int BK_, int WM_, int WN_> struct Tile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
@@ -50,11 +54,10 @@ template <int BM_, int BN_, int BK_, int WM_, int WN_> struct Tile {
     static constexpr int STAGE = A_STAGE + B_STAGE;
     static constexpr int A_ITEMS = BM * KQ / THREADS;
     static constexpr int B_ITEMS = KQ * (BN / 4) / THREADS;
+    static constexpr int BN_ITEMS = BN * KQ / THREADS; // B as pixel rows (LOAD_NHWC)
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
     static_assert(BK % 8 == 0, "BK must be a multiple of 8");
     static_assert((BM * KQ) % THREADS == 0, "A stage must split evenly over threads");
-    static_assert((KQ * (BN / 4)) % THREADS == 0, "B stage must split evenly over threads");
-    static_assert(THREADS % (BN / 4) == 0 || (BN / 4) % THREADS == 0, "B column mapping");
 };
 
 struct GemmArgs {
@@ -68,8 +71,9 @@ struct GemmArgs {
     int lda, ldb, ldc;
     int k_per_split;  // multiple of BK
     int flags;
-    // conv geometry (N = batch * P columns)
+    // conv geometry (N = batch * P columns); Cin, KW only for LOAD_NHWC
     int P, OW, H, W, CHW, stride, pad;
+    int Cin, KW;
 };
 
 __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
@@ -101,8 +105,41 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     const int kend = min(g.K, kbeg + g.k_per_split);
     const int nk = kend > kbeg ? (kend - kbeg + T::BK - 1) / T::BK : 0;
 
+    if constexpr (BMODE == LOAD_NHWC) {
+        static_assert((T::BN * T::KQ) % T::THREADS == 0, "B pixel rows must split evenly");
+    } else {
+        static_assert((T::KQ * (T::BN / 4)) % T::THREADS == 0, "B stage must split evenly");
+        static_assert(T::THREADS % (T::BN / 4) == 0 || (T::BN / 4) % T::THREADS == 0,
+                      "B column mapping");
+    }
     float4 ra[T::A_ITEMS];
-    float4 rb[T::B_ITEMS][4];
+    float4 rb[BMODE == LOAD_NHWC ? 1 : T::B_ITEMS][4];
+    float4 rbn[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
+
+    // ---- NHWC conv: each thread's B items are fixed (pixel, k-quad) pairs.
+    // Pixel geometry is decoded once; the k-quad's (kh, kw, c) comes from the
+    // stage start (uniform: one stage never crosses a (kh, kw) boundary).
+    int px_base[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
+    int px_ih[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
+    int px_iw[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
+    if constexpr (BMODE == LOAD_NHWC) {
+#pragma unroll
+        for (int i = 0; i < T::BN_ITEMS; ++i) {
+            const int q = tid + i * T::THREADS;
+            const int pg = n0 + q / T::KQ;
+            if (pg < g.N) {
+                const int img = pg / g.P, p = pg - img * g.P;
+                const int oh = p / g.OW, ow = p - oh * g.OW;
+                px_ih[i] = oh * g.stride - g.pad;
+                px_iw[i] = ow * g.stride - g.pad;
+                px_base[i] = ((img * g.H + px_ih[i]) * g.W + px_iw[i]) * g.Cin;
+            } else {
+                px_ih[i] = -(1 << 28); // never in range
+                px_iw[i] = 0;
+                px_base[i] = 0;
+            }
+        }
+    }
 
     // ---- conv: per-thread column geometry, fixed for the whole K loop ----
     // Column c of the thread's 4 columns is n0 + nq + c*(BN/4) (spread so a
@@ -146,8 +183,23 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 ra[i].w = (rv && gk + 3 < kend) ? src[3] : 0.f;
             }
         }
+        if constexpr (BMODE == LOAD_NHWC) {
+            // k0 .. k0+BK-1 share (kh, kw): channels c0 .. c0+BK-1.
+            const int khw = k0 / g.Cin, c0 = k0 - khw * g.Cin;
+            const int kh = khw / g.KW, kw = khw - kh * g.KW;
+            const int koff = (kh * g.W + kw) * g.Cin + c0;
 #pragma unroll
-        for (int i = 0; i < T::B_ITEMS; ++i) {
+            for (int i = 0; i < T::BN_ITEMS; ++i) {
+                const int q = tid + i * T::THREADS;
+                const int kq = q % T::KQ;
+                const int ih = px_ih[i] + kh, iw = px_iw[i] + kw;
+                rbn[i] = ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W && k0 < kend)
+                             ? *reinterpret_cast<const float4 *>(g.B + (size_t)(px_base[i] + koff) + 4 * kq)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (BMODE == LOAD_NHWC ? 0 : T::B_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
             if constexpr (BMODE == LOAD_VEC) {
@@ -200,8 +252,16 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             const int kq = q % T::KQ, m = q / T::KQ;
             *reinterpret_cast<float4 *>(As + kq * T::A_PLANE + m * 4) = ra[i];
         }
+        if constexpr (BMODE == LOAD_NHWC) {
 #pragma unroll
-        for (int i = 0; i < T::B_ITEMS; ++i) {
+            for (int i = 0; i < T::BN_ITEMS; ++i) {
+                const int q = tid + i * T::THREADS;
+                const int kq = q % T::KQ, n = q / T::KQ;
+                *reinterpret_cast<float4 *>(Bs + kq * T::B_PLANE + n * 4) = rbn[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (BMODE == LOAD_NHWC ? 0 : T::B_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
             float *plane = Bs + kq * T::B_PLANE;
@@ -278,11 +338,11 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         const int col = n0 + wn * T::WTN + j * 32 + r32;
         if (col >= g.N) continue;
         size_t col_off = col;
-        if constexpr (BMODE == LOAD_CONV) {
+        if constexpr (is_conv<BMODE>) {
             const int img = col / g.P, p = col - img * g.P;
             col_off = (size_t)img * g.M * g.P + p;
         }
-        const float bias_col = (has_bias && BMODE != LOAD_CONV) ? g.bias[col] : 0.f;
+        const float bias_col = (has_bias && !is_conv<BMODE>) ? g.bias[col] : 0.f;
 #pragma unroll
         for (int i = 0; i < T::FM; ++i) {
 #pragma unroll
@@ -294,9 +354,9 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                     g.partial[(size_t)blockIdx.y * g.M * g.N + (size_t)row * g.N + col] = x;
                     continue;
                 }
-                if (has_bias) x = x + (BMODE == LOAD_CONV ? g.bias[row] : bias_col);
+                if (has_bias) x = x + (is_conv<BMODE> ? g.bias[row] : bias_col);
                 if (has_relu) x = relu_idiom(x);
-                if constexpr (BMODE == LOAD_CONV)
+                if constexpr (is_conv<BMODE>)
                     g.C[col_off + (size_t)row * g.P] = x;
                 else
                     g.C[(size_t)row * g.ldc + col] = x;
@@ -335,14 +395,118 @@ __global__ void matmul_generic_kernel(int adt, const void *A, int bdt, const voi
     }
 }
 
+// ---- conv helpers ----------------------------------------------------------------
+
+// x [N][C][HW] -> xt [N][HW][C]: 32x32 tiles through LDS, one image per z.
+__global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const float *__restrict__ x,
+                                                           float *__restrict__ xt, int C, int HW) {
+    __shared__ float tile[32][33];
+    const size_t img = blockIdx.z;
+    const float *src = x + img * (size_t)C * HW;
+    float *dst = xt + img * (size_t)C * HW;
+    const int p0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+    for (int k = ty; k < 32; k += 8) {
+        const int c = c0 + k, p = p0 + tx;
+        if (c < C && p < HW) tile[k][tx] = src[(size_t)c * HW + p];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = ty; k < 32; k += 8) {
+        const int p = p0 + k, c = c0 + tx;
+        if (c < C && p < HW) dst[(size_t)p * C + c] = tile[tx][k];
+    }
+}
+
+// w [Co][C][KH][KW] -> wt [Co][KH][KW][C] (K ordered (kh, kw, c)).
+__global__ void weights_khwc_kernel(const float *__restrict__ w, float *__restrict__ wt, int Co,
+                                    int C, int KHW) {
+    const int total = Co * C * KHW;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int co = i / (C * KHW), r = i - co * C * KHW;
+        const int c = r / KHW, khw = r - c * KHW;
+        wt[(size_t)co * C * KHW + (size_t)khw * C + c] = w[i];
+    }
+}
+
+// Direct convolution for a tiny reduction (C*KH*KW <= DIRECT_MAX_K, e.g. the
+// first layer of an image CNN with C = 1): one thread per output pixel and
+// DIRECT_CO output channels; the weights of the block's channels sit in LDS.
+// Accumulation runs in k = (c, kh, kw) ascending order with fp32 FMA, the
+// same order as the GEMM path; bias then relu as x * (x > 0).
+constexpr int DIRECT_MAX_K = 32;
+constexpr int DIRECT_CO = 8;
+
+// KMAX >= C*KH*KW: the k loops unroll over KMAX so the patch stays in registers.
+template <int KMAX>
+__global__ __launch_bounds__(256) void conv2d_direct_kernel(
+    const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
+    float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
+    int stride, int pad, int flags) {
+    __shared__ float ws[DIRECT_CO * KMAX];
+    const int K = C * KH * KW;
+    const int co0 = blockIdx.y * DIRECT_CO;
+    for (int i = threadIdx.x; i < DIRECT_CO * KMAX; i += blockDim.x) {
+        const int co = co0 + i / KMAX, k = i % KMAX;
+        ws[i] = (co < Co && k < K) ? w[(size_t)co * K + k] : 0.f;
+    }
+    __syncthreads();
+    const int pg = blockIdx.x * blockDim.x + threadIdx.x;
+    if (pg >= NP) return;
+    const int img = pg / P, p = pg - img * P;
+    const int oh = p / OW, ow = p - oh * OW;
+    const int ih0 = oh * stride - pad, iw0 = ow * stride - pad;
+    const float *xi = x + (size_t)img * C * H * W;
+    float xv[KMAX];
+    int c = 0, kh = 0, kw = 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        float v = 0.f;
+        if (k < K) {
+            const int ih = ih0 + kh, iw = iw0 + kw;
+            if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                v = xi[(size_t)c * H * W + (size_t)ih * W + iw];
+            if (++kw == KW) {
+                kw = 0;
+                if (++kh == KH) {
+                    kh = 0;
+                    ++c;
+                }
+            }
+        }
+        xv[k] = v;
+    }
+#pragma unroll
+    for (int j = 0; j < DIRECT_CO; ++j) {
+        const int co = co0 + j;
+        if (co >= Co) break;
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k)
+            if (k < K) acc = __builtin_fmaf(ws[j * KMAX + k], xv[k], acc);
+        if (flags & CAMEL_EPI_BIAS) acc = acc + bias[co];
+        if (flags & CAMEL_EPI_RELU) acc = relu_idiom(acc);
+        y[((size_t)img * Co + co) * P + p] = acc;
+    }
+}
+
 // ---- host-side launch -----------------------------------------------------------
 
-using TileBig = Tile<256, 256, 16, 2, 2>;   // wave 128x128
-using TileMid = Tile<128, 128, 32, 2, 2>;   // wave 64x64
-using TileSmall = Tile<64, 64, 64, 2, 2>;   // wave 32x32
-using TileSkinny = Tile<32, 256, 32, 1, 4>; // wave 32x64
-using TileConv = Tile<128, 256, 16, 2, 2>;  // wave 64x128
-using TileConv64 = Tile<64, 256, 32, 1, 4>; // wave 64x64
+// Tile shapes, chosen by measured sweeps on MI355X (GEMM 1024-8192, the
+// BASELINE conv shapes): 8 waves at 256x256 keep the accumulators in arch
+// VGPRs without spills; the conv tiles are small enough for two work-groups
+// per CU, which hides the gather latency better than larger tiles do.
+using TileBig = Tile<256, 256, 32, 2, 4>;    // wave 128x64, 8 waves
+using TileMid = Tile<128, 128, 32, 2, 2>;    // wave 64x64
+using TileSmall = Tile<64, 64, 64, 2, 2>;    // wave 32x32
+using TileSkinny = Tile<32, 128, 64, 1, 4>;  // wave 32x32, M <= 32
+using TileConv = Tile<128, 128, 32, 2, 2>;   // NHWC conv, Co > 64, C % 32 == 0
+using TileConv16 = Tile<128, 128, 16, 2, 2>; // NHWC conv, Co > 64, C % 16 == 0
+using TileConv64 = Tile<64, 128, 32, 2, 2>;  // NHWC conv, Co <= 64, C % 32 == 0
+using TileConv64k16 = Tile<64, 128, 16, 2, 2>; // NHWC conv, Co <= 64, C % 16 == 0
+using TileGather = Tile<128, 256, 16, 2, 2>;   // NCHW gather conv, Co > 64
+using TileGather64 = Tile<64, 256, 32, 1, 4>;  // NCHW gather conv, Co <= 64
 
 template <class T> int64_t tiles_of(int64_t M, int64_t N) {
     return ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
@@ -398,6 +562,9 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
     } else if (tiles_of<TileMid>(M, N) >= cus) {
         cfg = Cfg::Mid;
         bk = TileMid::BK;
+        // One tile per CU leaves the MFMA pipes half fed; a 2-way K split of
+        // long reductions measured 8% faster at 2048^3.
+        if (tiles_of<TileMid>(M, N) < 2 * cus && K >= 2048) splits = 2;
         return;
     } else {
         cfg = Cfg::Small;
@@ -409,6 +576,139 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
     const int64_t want = (cus + tiles - 1) / tiles;
     const int64_t max_splits = std::max<int64_t>(1, K / (4 * bk));
     splits = (int)std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(max_splits, 64)));
+}
+
+// ---- conv2d host paths -----------------------------------------------------------
+
+int conv2d_direct(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
+                  int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
+                  int64_t pad, int64_t OH, int64_t OW, int flags) {
+    const int64_t P = OH * OW, NP = N * P;
+    const int64_t K = C * KH * KW;
+    dim3 grid((unsigned)((NP + 255) / 256), (unsigned)((Co + DIRECT_CO - 1) / DIRECT_CO));
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream(), x, w, bias, y, (int)NP, (int)P,
+                           (int)OW, (int)C, (int)H, (int)W, (int)Co, (int)KH, (int)KW, (int)stride,
+                           (int)pad, flags);
+        return check_launch("conv2d_direct_kernel");
+    };
+    if (K <= 9)
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<9>));
+    else if (K <= 16)
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<16>));
+    else
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<DIRECT_MAX_K>));
+    return ok();
+}
+
+GemmArgs conv_args(const float *w, const float *x, const float *bias, float *y, int64_t N,
+                   int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
+                   int64_t stride, int64_t pad, int64_t OH, int64_t OW, int flags) {
+    GemmArgs g{};
+    g.A = w;
+    g.B = x;
+    g.C = y;
+    g.bias = bias;
+    g.M = (int)Co;
+    g.N = (int)(N * OH * OW);
+    g.K = (int)(C * KH * KW);
+    g.lda = g.K;
+    g.flags = flags;
+    g.P = (int)(OH * OW);
+    g.OW = (int)OW;
+    g.H = (int)H;
+    g.W = (int)W;
+    g.CHW = (int)(C * H * W);
+    g.stride = (int)stride;
+    g.pad = (int)pad;
+    g.Cin = (int)C;
+    g.KW = (int)KW;
+    return g;
+}
+
+// NHWC implicit GEMM: x is transposed to NHWC and w reordered to (kh, kw, c)
+// in pooled scratch (stream-ordered, returned to the pool after the launch).
+template <class T>
+int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
+                int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
+                int64_t pad, int64_t OH, int64_t OW, int flags) {
+    const int64_t HW = H * W, K = C * KH * KW;
+    void *xt = nullptr, *wt = nullptr;
+    CAMEL_RETURN_IF(camel_hip_malloc(&xt, (size_t)(N * C * HW) * sizeof(float)));
+    int rc = camel_hip_malloc(&wt, (size_t)(Co * K) * sizeof(float));
+    if (rc == CAMEL_HIP_OK) {
+        dim3 tgrid((unsigned)((HW + 31) / 32), (unsigned)((C + 31) / 32), (unsigned)N);
+        hipLaunchKernelGGL(nchw_to_nhwc_kernel, tgrid, dim3(256), 0, stream(), x,
+                           static_cast<float *>(xt), (int)C, (int)HW);
+        rc = check_launch("nchw_to_nhwc_kernel");
+    }
+    if (rc == CAMEL_HIP_OK) {
+        hipLaunchKernelGGL(weights_khwc_kernel, dim3(grid_for(Co * K, 256)), dim3(256), 0, stream(),
+                           w, static_cast<float *>(wt), (int)Co, (int)C, (int)(KH * KW));
+        rc = check_launch("weights_khwc_kernel");
+    }
+    if (rc == CAMEL_HIP_OK) {
+        GemmArgs g = conv_args(static_cast<const float *>(wt), static_cast<const float *>(xt), bias,
+                               y, N, C, H, W, Co, KH, KW, stride, pad, OH, OW, flags);
+        g.k_per_split = g.K;
+        rc = launch<T, LOAD_VEC, LOAD_NHWC>(g, 1, "conv2d_nhwc_kernel");
+    }
+    camel_hip_free(wt);
+    camel_hip_free(xt);
+    CAMEL_RETURN_IF(rc);
+    return ok();
+}
+
+// General path: im2col columns gathered from NCHW x through a k -> (c, kh, kw)
+// offset table built on the host once per geometry.
+int conv2d_gather(const float *x, const float *w, const float *bias, float *y, int64_t N,
+                  int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
+                  int64_t stride, int64_t pad, int64_t OH, int64_t OW, int flags) {
+    const int64_t K = C * KH * KW;
+    static std::vector<int2> host_tab;
+    static int2 *dev_tab = nullptr;
+    static int64_t tab_cap = 0;
+    static int64_t tab_key[4] = {-1, -1, -1, -1};
+    if (tab_key[0] != C || tab_key[1] != KH || tab_key[2] != KW || tab_key[3] != H * W * 65536 + W) {
+        if (K > tab_cap) {
+            if (dev_tab) {
+                CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+                camel_hip_free(dev_tab);
+            }
+            void *p = nullptr;
+            CAMEL_RETURN_IF(camel_hip_malloc(&p, (size_t)K * sizeof(int2)));
+            dev_tab = static_cast<int2 *>(p);
+            tab_cap = K;
+        }
+        host_tab.resize((size_t)K);
+        for (int64_t k = 0; k < K; ++k) {
+            const int64_t c = k / (KH * KW), r = k % (KH * KW), kh = r / KW, kw = r % KW;
+            host_tab[(size_t)k] = make_int2((int)(c * H * W + kh * W + kw), (int)((kh << 16) | kw));
+        }
+        CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dev_tab, host_tab.data(), (size_t)K * sizeof(int2),
+                                                 hipMemcpyHostToDevice, stream()),
+                                  "hipMemcpyAsync(conv table)"));
+        CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+        tab_key[0] = C;
+        tab_key[1] = KH;
+        tab_key[2] = KW;
+        tab_key[3] = H * W * 65536 + W;
+    }
+    GemmArgs g = conv_args(w, x, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH, OW, flags);
+    g.ktab = dev_tab;
+    const bool avec = (K % 4 == 0) && ((uintptr_t)w % 16 == 0);
+    int rc;
+    if (Co <= 64) {
+        g.k_per_split = (int)((K + TileGather64::BK - 1) / TileGather64::BK * TileGather64::BK);
+        rc = avec ? launch<TileGather64, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
+                  : launch<TileGather64, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
+    } else {
+        g.k_per_split = (int)((K + TileGather::BK - 1) / TileGather::BK * TileGather::BK);
+        rc = avec ? launch<TileGather, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
+                  : launch<TileGather, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
+    }
+    CAMEL_RETURN_IF(rc);
+    return ok();
 }
 
 } // namespace
@@ -511,67 +811,22 @@ int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y
     if (!x || !w || !y) return fail(CAMEL_HIP_ERR_ARG, "conv2d: null operand");
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
-    // k -> (c, kh, kw) table, built on the host once per geometry.
-    static std::vector<int2> host_tab;
-    static int2 *dev_tab = nullptr;
-    static int64_t tab_cap = 0;
-    static int64_t tab_key[4] = {-1, -1, -1, -1};
-    if (tab_key[0] != C || tab_key[1] != KH || tab_key[2] != KW || tab_key[3] != H * W * 65536 + W) {
-        if (K > tab_cap) {
-            if (dev_tab) {
-                CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
-                camel_hip_free(dev_tab);
-            }
-            void *p = nullptr;
-            CAMEL_RETURN_IF(camel_hip_malloc(&p, (size_t)K * sizeof(int2)));
-            dev_tab = static_cast<int2 *>(p);
-            tab_cap = K;
-        }
-        host_tab.resize((size_t)K);
-        for (int64_t k = 0; k < K; ++k) {
-            const int64_t c = k / (KH * KW), r = k % (KH * KW), kh = r / KW, kw = r % KW;
-            host_tab[(size_t)k] = make_int2((int)(c * H * W + kh * W + kw), (int)((kh << 16) | kw));
-        }
-        CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dev_tab, host_tab.data(), (size_t)K * sizeof(int2),
-                                                 hipMemcpyHostToDevice, stream()),
-                                  "hipMemcpyAsync(conv table)"));
-        CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
-        tab_key[0] = C;
-        tab_key[1] = KH;
-        tab_key[2] = KW;
-        tab_key[3] = H * W * 65536 + W;
+    if (K <= DIRECT_MAX_K) return conv2d_direct(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
+                                                OW, flags);
+    const bool aligned = (((uintptr_t)x | (uintptr_t)w) & 15) == 0;
+    if (aligned && C % 16 == 0) {
+        const bool k32 = C % 32 == 0;
+        if (Co > 64)
+            return k32 ? conv2d_nhwc<TileConv>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
+                                              OW, flags)
+                       : conv2d_nhwc<TileConv16>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad,
+                                                OH, OW, flags);
+        return k32 ? conv2d_nhwc<TileConv64>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
+                                            OW, flags)
+                   : conv2d_nhwc<TileConv64k16>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad,
+                                               OH, OW, flags);
     }
-    GemmArgs g{};
-    g.A = w;
-    g.B = x;
-    g.C = y;
-    g.bias = bias;
-    g.ktab = dev_tab;
-    g.M = (int)Co;
-    g.N = (int)NP;
-    g.K = (int)K;
-    g.lda = (int)K;
-    g.flags = flags;
-    g.P = (int)P;
-    g.OW = (int)OW;
-    g.H = (int)H;
-    g.W = (int)W;
-    g.CHW = (int)(C * H * W);
-    g.stride = (int)stride;
-    g.pad = (int)pad;
-    const bool avec = (K % 4 == 0) && ((uintptr_t)w % 16 == 0);
-    int rc;
-    if (Co <= 64) {
-        g.k_per_split = (int)((K + TileConv64::BK - 1) / TileConv64::BK * TileConv64::BK);
-        rc = avec ? launch<TileConv64, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
-                  : launch<TileConv64, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
-    } else {
-        g.k_per_split = (int)((K + TileConv::BK - 1) / TileConv::BK * TileConv::BK);
-        rc = avec ? launch<TileConv, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
-                  : launch<TileConv, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
-    }
-    CAMEL_RETURN_IF(rc);
-    return ok();
+    return conv2d_gather(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH, OW, flags);
 }
 
 } // extern "C"

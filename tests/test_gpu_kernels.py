@@ -294,6 +294,27 @@ def test_conv2d_matches_oracle(N, Cin, H_, W_, Co, k, stride, pad):
     assert conv_bound_ok(got, ref, x, w, stride, pad)
 
 
+@pytest.mark.parametrize("N,Cin,H_,W_,Co,kh,kw,stride,pad", [
+    (2, 64, 17, 15, 96, 3, 3, 2, 1),    # NHWC path, 128-row tile, stride 2, ragged tiles
+    (3, 32, 12, 10, 40, 3, 5, 1, 2),    # NHWC path, 64-row tile, KH != KW, wide pad
+    (1, 64, 9, 9, 200, 1, 1, 1, 0),     # NHWC path, 1x1 kernel, two row tiles
+    (2, 48, 7, 7, 150, 3, 3, 1, 1),     # NHWC path with C = 48 (3 stages per (kh, kw))
+    (2, 12, 8, 8, 24, 3, 3, 1, 1),      # gather path: C % 16 != 0, K = 108
+    (4, 2, 10, 10, 33, 4, 4, 2, 1),     # direct path, K = 32, Co not a multiple of 8
+])
+def test_conv2d_paths_rect_kernels(N, Cin, H_, W_, Co, kh, kw, stride, pad):
+    x = D.normal(910 + Cin, (N, Cin, H_, W_))
+    w = D.normal(911 + Co, (Co, Cin, kh, kw)) * F(np.sqrt(2.0 / (kh * kw * Cin)))
+    b = D.uniform(912, (Co,), -0.1, 0.1)
+    for flags, relu in ((H.EPI_BIAS | H.EPI_RELU, True), (0, False)):
+        ref = O.conv2d(x, w, b if flags else None, relu, stride, pad)
+        dx, dw, db, dy = K.dev(x), K.dev(w), K.dev(b), K.empty(ref.nbytes)
+        H.call("camel_hip_conv2d", P(dx.ptr), P(dw.ptr), P(db.ptr) if flags else None, P(dy.ptr), N,
+               Cin, H_, W_, Co, kh, kw, stride, pad, flags)
+        got = K.host(dy, F, ref.shape)
+        assert conv_bound_ok(got, ref, x, w, stride, pad)
+
+
 def test_conv2d_full_config_slab():
     # BASELINE config 4 at full size; the oracle checks images 0 and 63
     x = D.normal(D.SEED_CONV_X, (64, 64, 56, 56))
