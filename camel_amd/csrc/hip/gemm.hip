@@ -25,6 +25,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 namespace camel_hip {
@@ -65,30 +66,39 @@ struct GemmArgs {
     const float *B;  // [K, ldb] row-major (conv: input x, NCHW)
     float *C;        // [M, ldc] row-major (conv: output y, NCHW)
     const float *bias;
-    float *partial;  // split-K partials [splits][M][N], or null
+    float *partial;  // split-K partials [split][tile of launch][BM * BN], or null
     const int2 *ktab; // conv: per k {offset of (c,kh,kw) in x, kh << 16 | kw}
     int M, N, K;
     int lda, ldb, ldc;
     int k_per_split;  // multiple of BK
+    int tile_begin;   // first logical tile of the launch
     int flags;
     // conv geometry (N = batch * P columns); Cin, KW only for LOAD_NHWC
     int P, OW, H, W, CHW, stride, pad;
     int Cin, KW;
 };
 
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
-    int bid = blockIdx.x;
-    const int nb = gridDim.x;
-    // Workgroups are dispatched round-robin over the 8 XCDs: give XCD x the
-    // contiguous id range [x*nb/8, (x+1)*nb/8) so its L2 sees a compact block.
-    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+// Logical tile id -> (tm, tn), grouped GROUP_M tile-rows deep so that
+// consecutive ids share B panels.  A bijection on [0, tiles_m * tiles_n).
+__device__ __forceinline__ void tile_of(int id, int tiles_m, int tiles_n, int &tm, int &tn) {
     const int per_group = GROUP_M * tiles_n;
-    const int g = bid / per_group;
+    const int g = id / per_group;
     const int first_m = g * GROUP_M;
     const int gsize = min(tiles_m - first_m, GROUP_M);
-    const int in_group = bid - g * per_group;
+    const int in_group = id - g * per_group;
     tm = first_m + in_group % gsize;
     tn = in_group / gsize;
+}
+
+// Logical tile of this work-group.  A launch covers tiles [tile_begin,
+// tile_begin + gridDim.x); blockIdx.y is the K split.  Work-groups are
+// dispatched round-robin over the 8 XCDs, so a single-split launch gives XCD x
+// the contiguous id range [x*nb/8, (x+1)*nb/8) and its L2 a compact block.
+__device__ __forceinline__ int block_tile_id(int tile_begin) {
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if (gridDim.y == 1 && (nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    return tile_begin + bid;
 }
 
 template <class T, int AMODE, int BMODE>
@@ -99,7 +109,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     const int tiles_m = (g.M + T::BM - 1) / T::BM;
     const int tiles_n = (g.N + T::BN - 1) / T::BN;
     int tm, tn;
-    tile_coords(tiles_m, tiles_n, tm, tn);
+    tile_of(block_tile_id(g.tile_begin), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * T::BM, n0 = tn * T::BN;
     const int kbeg = blockIdx.y * g.k_per_split;
     const int kend = min(g.K, kbeg + g.k_per_split);
@@ -112,9 +122,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         static_assert(T::THREADS % (T::BN / 4) == 0 || (T::BN / 4) % T::THREADS == 0,
                       "B column mapping");
     }
-    float4 ra[T::A_ITEMS];
-    float4 rb[BMODE == LOAD_NHWC ? 1 : T::B_ITEMS][4];
-    float4 rbn[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
+    // One stage of operands in flight from global memory to LDS.
+    struct StageRegs {
+        float4 ra[T::A_ITEMS];
+        float4 rb[BMODE == LOAD_NHWC ? 1 : T::B_ITEMS][4];
+        float4 rbn[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
+    };
+    StageRegs R0;
 
     // ---- NHWC conv: each thread's B items are fixed (pixel, k-quad) pairs.
     // Pixel geometry is decoded once; the k-quad's (kh, kw, c) comes from the
@@ -165,7 +179,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         }
     }
 
-    auto load_stage = [&](int k0) {
+    // FULL: the tile lies inside M x N and every stage is a whole BK of K, so
+    // the row/column/k guards compile away (interior tiles of most problems).
+    auto load_stage = [&](auto full_tag, int k0, StageRegs &R) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        float4 *ra = R.ra;
+        auto &rb = R.rb;
+        float4 *rbn = R.rbn;
 #pragma unroll
         for (int i = 0; i < T::A_ITEMS; ++i) {
             const int q = tid + i * T::THREADS;
@@ -173,14 +193,14 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             const int gm = m0 + m, gk = k0 + 4 * kq;
             const float *src = g.A + (size_t)gm * g.lda + gk;
             if constexpr (AMODE == LOAD_VEC) {
-                ra[i] = (gm < g.M && gk < kend) ? *reinterpret_cast<const float4 *>(src)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                ra[i] = (FULL || (gm < g.M && gk < kend)) ? *reinterpret_cast<const float4 *>(src)
+                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
-                const bool rv = gm < g.M;
-                ra[i].x = (rv && gk + 0 < kend) ? src[0] : 0.f;
-                ra[i].y = (rv && gk + 1 < kend) ? src[1] : 0.f;
-                ra[i].z = (rv && gk + 2 < kend) ? src[2] : 0.f;
-                ra[i].w = (rv && gk + 3 < kend) ? src[3] : 0.f;
+                const bool rv = FULL || gm < g.M;
+                ra[i].x = (rv && (FULL || gk + 0 < kend)) ? src[0] : 0.f;
+                ra[i].y = (rv && (FULL || gk + 1 < kend)) ? src[1] : 0.f;
+                ra[i].z = (rv && (FULL || gk + 2 < kend)) ? src[2] : 0.f;
+                ra[i].w = (rv && (FULL || gk + 3 < kend)) ? src[3] : 0.f;
             }
         }
         if constexpr (BMODE == LOAD_NHWC) {
@@ -193,7 +213,8 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 const int q = tid + i * T::THREADS;
                 const int kq = q % T::KQ;
                 const int ih = px_ih[i] + kh, iw = px_iw[i] + kw;
-                rbn[i] = ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W && k0 < kend)
+                rbn[i] = ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W &&
+                          (FULL || k0 < kend))
                              ? *reinterpret_cast<const float4 *>(g.B + (size_t)(px_base[i] + koff) + 4 * kq)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
             }
@@ -207,7 +228,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
-                    rb[i][u] = (gn < g.N && gk < kend)
+                    rb[i][u] = (FULL || (gn < g.N && gk < kend))
                                    ? *reinterpret_cast<const float4 *>(g.B + (size_t)gk * g.ldb + gn)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
@@ -220,7 +241,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         const int gn = n0 + nq + c * (T::BN / 4);
-                        v[c] = (gn < g.N && gk < kend) ? row[gn] : 0.f;
+                        v[c] = (FULL || (gn < g.N && gk < kend)) ? row[gn] : 0.f;
                     }
                     rb[i][u] = make_float4(v[0], v[1], v[2], v[3]);
                 }
@@ -229,7 +250,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
                     float v[4] = {0.f, 0.f, 0.f, 0.f};
-                    if (gk < kend) {
+                    if (FULL || gk < kend) {
                         const int2 e = g.ktab[gk];
                         const int kh = e.y >> 16, kw = e.y & 0xffff;
 #pragma unroll
@@ -245,7 +266,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         }
     };
 
-    auto store_stage = [&](float *As, float *Bs) {
+    auto store_stage = [&](float *As, float *Bs, const StageRegs &R) {
+        const float4 *ra = R.ra;
+        const auto &rb = R.rb;
+        const float4 *rbn = R.rbn;
 #pragma unroll
         for (int i = 0; i < T::A_ITEMS; ++i) {
             const int q = tid + i * T::THREADS;
@@ -292,43 +316,67 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    if (nk > 0) {
-        load_stage(kbeg);
-        store_stage(smem, smem + T::A_STAGE);
-        __syncthreads();
-    }
-
-    for (int kt = 0; kt < nk; ++kt) {
-        const bool more = kt + 1 < nk;
-        if (more) load_stage(kbeg + (kt + 1) * T::BK);
+    // LDS operand reads run one 8-k group ahead of the MFMAs that use them, so
+    // each group's ds_read latency hides behind the previous group's MFMAs.
+    auto compute_stage = [&](int kt) {
         const float *As = smem + (kt & 1) * T::STAGE;
         const float *Bs = As + T::A_STAGE;
         const float *a_base = As + half * T::A_PLANE + (wm * T::WTM + r32) * 4;
         const float *b_base = Bs + half * T::B_PLANE + (wn * T::WTN + r32) * 4;
-#pragma unroll
-        for (int s8 = 0; s8 < T::BK / 8; ++s8) {
-            float4 a[T::FM], b[T::FN];
+        constexpr int GROUPS = T::BK / 8;
+        float4 a[2][T::FM], b[2][T::FN];
+        auto fetch = [&](int s8, float4 *fa, float4 *fb) {
 #pragma unroll
             for (int i = 0; i < T::FM; ++i)
-                a[i] = *reinterpret_cast<const float4 *>(a_base + 2 * s8 * T::A_PLANE + i * 128);
+                fa[i] = *reinterpret_cast<const float4 *>(a_base + 2 * s8 * T::A_PLANE + i * 128);
 #pragma unroll
             for (int j = 0; j < T::FN; ++j)
-                b[j] = *reinterpret_cast<const float4 *>(b_base + 2 * s8 * T::B_PLANE + j * 128);
+                fb[j] = *reinterpret_cast<const float4 *>(b_base + 2 * s8 * T::B_PLANE + j * 128);
+        };
+        fetch(0, a[0], b[0]);
+        __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
+#pragma unroll
+        for (int s8 = 0; s8 < GROUPS; ++s8) {
+            const int cur = s8 & 1;
+            if (s8 + 1 < GROUPS) fetch(s8 + 1, a[cur ^ 1], b[cur ^ 1]);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int i = 0; i < T::FM; ++i)
 #pragma unroll
                     for (int j = 0; j < T::FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t],
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][i][t], b[cur][j][t],
                                                                           acc[i][j], 0, 0, 0);
+            // Keep the order above: the next group's LDS reads issue before
+            // this group's MFMAs (masks: 0x100 LDS read, 0x8 MFMA).
+            if (s8 + 1 < GROUPS) __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
         }
-        if (more) {
-            float *nxt = smem + ((kt + 1) & 1) * T::STAGE;
-            store_stage(nxt, nxt + T::A_STAGE);
+    };
+    auto lds_stage = [&](int kt) { return smem + (kt & 1) * T::STAGE; };
+
+    // Stage kt+1 is fetched into registers while stage kt is multiplied, then
+    // stored to the other LDS buffer; one barrier per stage.
+    auto main_loop = [&](auto full_tag) {
+        if (nk > 0) {
+            load_stage(full_tag, kbeg, R0);
+            store_stage(smem, smem + T::A_STAGE, R0);
+            __syncthreads();
         }
-        __syncthreads();
-    }
+        for (int kt = 0; kt < nk; ++kt) {
+            const bool more = kt + 1 < nk;
+            if (more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0);
+            compute_stage(kt);
+            if (more) store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
+            __syncthreads();
+        }
+    };
+    const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N) &&
+                           (kend - kbeg) % T::BK == 0;
+    if (full_tile)
+        main_loop(std::true_type{});
+    else
+        main_loop(std::false_type{});
 
     // ---- epilogue ----
     const bool has_bias = (g.flags & CAMEL_EPI_BIAS) != 0 && g.partial == nullptr;
@@ -351,7 +399,8 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 if (row >= g.M) continue;
                 float x = acc[i][j][v];
                 if (g.partial) {
-                    g.partial[(size_t)blockIdx.y * g.M * g.N + (size_t)row * g.N + col] = x;
+                    g.partial[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (T::BM * T::BN) +
+                              (size_t)(row - m0) * T::BN + (col - n0)] = x;
                     continue;
                 }
                 if (has_bias) x = x + (is_conv<BMODE> ? g.bias[row] : bias_col);
@@ -365,19 +414,149 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     }
 }
 
-// Sums split-K partials in split order, then bias and relu.
-__global__ void splitk_reduce_kernel(const float *partial, int splits, float *C, int M, int N,
-                                     int ldc, const float *bias, int flags) {
-    const size_t total = (size_t)M * N;
+// Sums the K splits of tiles [tile_begin, tile_begin + ntiles) in split
+// order (so results do not depend on scheduling), then bias and relu, and
+// stores with the GEMM (row-major) or conv (NCHW) output mapping.
+template <int BM, int BN, bool CONV>
+__global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles, int splits) {
+    const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+    const size_t per_tile = (size_t)BM * BN, total = (size_t)ntiles * per_tile;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
-        float s = partial[idx];
-        for (int z = 1; z < splits; ++z) s = s + partial[(size_t)z * total + idx];
-        const int row = (int)(idx / N), col = (int)(idx % N);
-        if (flags & CAMEL_EPI_BIAS) s = s + bias[col];
-        if (flags & CAMEL_EPI_RELU) s = relu_idiom(s);
-        C[(size_t)row * ldc + col] = s;
+        const int local = (int)(idx / per_tile);
+        const int w = (int)(idx - (size_t)local * per_tile);
+        int tm, tn;
+        tile_of(g.tile_begin + local, tiles_m, tiles_n, tm, tn);
+        const int row = tm * BM + w / BN, col = tn * BN + w % BN;
+        if (row >= g.M || col >= g.N) continue;
+        float s = g.partial[idx];
+        for (int z = 1; z < splits; ++z) s = s + g.partial[(size_t)z * total + idx];
+        if (g.flags & CAMEL_EPI_BIAS) s = s + (CONV ? g.bias[row] : g.bias[col]);
+        if (g.flags & CAMEL_EPI_RELU) s = relu_idiom(s);
+        if constexpr (CONV) {
+            const int img = col / g.P, p = col - img * g.P;
+            g.C[((size_t)img * g.M + row) * g.P + p] = s;
+        } else {
+            g.C[(size_t)row * g.ldc + col] = s;
+        }
     }
+}
+
+// Thin GEMM (N <= 32, e.g. a classifier layer 1024 -> 10): too few columns
+// for an MFMA tile to be useful.  B [K, N] is staged in LDS zero-padded to
+// [256 * KV][NT] (NT >= N), so the inner loops run without guards; rows are
+// STRIDE = NT + 4 floats apart so that the eight lanes one 16-byte LDS read
+// serves per cycle land on disjoint banks.  Each wave owns one row of A at a
+// time: lane l takes k = l + 64 i (coalesced loads, zero past K) and
+// accumulates all NT columns in fp32 FMA; a wave-shuffle tree sums the 64
+// partials; bias and relu as in the MFMA epilogue.
+constexpr int THIN_LDS_FLOATS = 20480; // 80 KiB of B per work-group
+
+template <int NT, int KV>
+__global__ __launch_bounds__(256) void sgemm_thin_kernel(const float *__restrict__ A,
+                                                         const float *__restrict__ B,
+                                                         float *__restrict__ C, int M, int N, int K,
+                                                         const float *__restrict__ bias, int flags) {
+    constexpr int STRIDE = NT + 4, ROWS = 256 * KV, KPL = ROWS / 64; // k per lane
+    static_assert(NT % 8 == 0 && ROWS * STRIDE <= THIN_LDS_FLOATS, "thin tile exceeds LDS");
+    __shared__ __attribute__((aligned(16))) float bs[ROWS * STRIDE];
+    const int lane = threadIdx.x & 63;
+    const int waves = gridDim.x * (blockDim.x >> 6);
+    auto load_row = [&](int m, float *av) {
+        const float *a = A + (size_t)m * K;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) {
+            const int k = lane + 64 * i;
+            av[i] = k < K ? a[k] : 0.f;
+        }
+    };
+    int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    float av[KPL];
+    // The first row's loads are in flight while B is staged (one batch of
+    // loads per thread, then the LDS stores).
+    if (m < M) load_row(m, av);
+    constexpr int PER_THREAD = ROWS * NT / 256, BATCH = PER_THREAD < 32 ? PER_THREAD : 32;
+    for (int base = 0; base < PER_THREAD; base += BATCH) {
+        float v[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int slot = (base + u) * 256 + (int)threadIdx.x;
+            const int k = slot / NT, n = slot % NT;
+            v[u] = (k < K && n < N) ? B[(size_t)k * N + n] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int slot = (base + u) * 256 + (int)threadIdx.x;
+            bs[(slot / NT) * STRIDE + slot % NT] = v[u];
+        }
+    }
+    __syncthreads();
+    for (; m < M; m += waves) {
+        float acc[NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[n] = 0.f;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) {
+            const float x = av[i];
+            const float4 *brow = reinterpret_cast<const float4 *>(bs + (lane + 64 * i) * STRIDE);
+#pragma unroll
+            for (int q = 0; q < NT / 4; ++q) {
+                const float4 bv = brow[q];
+                acc[4 * q + 0] = __builtin_fmaf(x, bv.x, acc[4 * q + 0]);
+                acc[4 * q + 1] = __builtin_fmaf(x, bv.y, acc[4 * q + 1]);
+                acc[4 * q + 2] = __builtin_fmaf(x, bv.z, acc[4 * q + 2]);
+                acc[4 * q + 3] = __builtin_fmaf(x, bv.w, acc[4 * q + 3]);
+            }
+        }
+        // The next row's loads overlap this row's reduction.
+        if (m + waves < M) load_row(m + waves, av);
+        float out = 0.f;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            float v = acc[n];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            out = lane == n ? v : out;
+        }
+        if (lane < N) {
+            if (flags & CAMEL_EPI_BIAS) out = out + bias[lane];
+            if (flags & CAMEL_EPI_RELU) out = relu_idiom(out);
+            C[(size_t)m * N + lane] = out;
+        }
+    }
+}
+
+// True when the thin kernel serves C[M, N] = A[M, K] B[K, N].
+bool thin_eligible(int64_t M, int64_t N, int64_t K) {
+    if (N > 32 || N * 8 >= M) return false;
+    // Longest k-slice per lane that the unrolled row loop holds in registers.
+    return K <= (N <= 16 ? 1024 : 512);
+}
+
+int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
+                int flags) {
+    // Enough waves to cover the rows once, at most one work-group per CU
+    // (each work-group stages all of B).
+    const unsigned blocks = (unsigned)std::max<int64_t>(
+        1, std::min<int64_t>((M + 3) / 4, device_cu_count()));
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), 0, stream(), A, B, C, M, N, K, bias,
+                           flags);
+        return check_launch("sgemm_thin_kernel");
+    };
+    const int kv = std::max(1, (K + 255) / 256);
+    if (N <= 8) {
+        if (kv <= 1) return go(sgemm_thin_kernel<8, 1>);
+        if (kv <= 2) return go(sgemm_thin_kernel<8, 2>);
+        return go(sgemm_thin_kernel<8, 4>);
+    }
+    if (N <= 16) {
+        if (kv <= 1) return go(sgemm_thin_kernel<16, 1>);
+        if (kv <= 2) return go(sgemm_thin_kernel<16, 2>);
+        return go(sgemm_thin_kernel<16, 4>);
+    }
+    if (kv <= 1) return go(sgemm_thin_kernel<32, 1>);
+    return go(sgemm_thin_kernel<32, 2>);
 }
 
 // Mixed-dtype matmul: one thread per output, double accumulation in k order
@@ -512,20 +691,6 @@ template <class T> int64_t tiles_of(int64_t M, int64_t N) {
     return ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
 }
 
-template <class T, int AMODE, int BMODE> int launch(GemmArgs g, int splits, const char *name) {
-    const int64_t tiles = tiles_of<T>(g.M, g.N);
-    dim3 grid((unsigned)tiles, (unsigned)splits);
-    hipLaunchKernelGGL((sgemm_kernel<T, AMODE, BMODE>), grid, dim3(T::THREADS), 0, stream(), g);
-    return check_launch(name);
-}
-
-template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool bvec) {
-    if (avec && bvec) return launch<T, LOAD_VEC, LOAD_VEC>(g, splits, "sgemm_kernel");
-    if (avec) return launch<T, LOAD_VEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
-    if (bvec) return launch<T, LOAD_SCALAR, LOAD_VEC>(g, splits, "sgemm_kernel");
-    return launch<T, LOAD_SCALAR, LOAD_SCALAR>(g, splits, "sgemm_kernel");
-}
-
 // Scratch for split-K partials, grown on demand (kept for the process).
 float *g_partial = nullptr;
 size_t g_partial_bytes = 0;
@@ -543,6 +708,74 @@ int ensure_partial(size_t bytes) {
     g_partial = static_cast<float *>(p);
     g_partial_bytes = bytes;
     return CAMEL_HIP_OK;
+}
+
+// Work-groups of one kernel that fit on the chip at once (occupancy x CUs).
+template <class T, int AMODE, int BMODE> int resident_slots() {
+    static int slots = 0;
+    if (slots == 0) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sgemm_kernel<T, AMODE, BMODE>,
+                                                         T::THREADS, 0) != hipSuccess ||
+            per_cu < 1)
+            per_cu = 1;
+        slots = per_cu * device_cu_count();
+    }
+    return slots;
+}
+
+// Runs tiles [tile_begin, tile_begin + ntiles) with `splits` K splits; split
+// launches write partials that tile_reduce_kernel folds into C.
+template <class T, int AMODE, int BMODE>
+int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char *name) {
+    g.tile_begin = tile_begin;
+    const int stages = (g.K + T::BK - 1) / T::BK;
+    splits = std::max(1, std::min(splits, stages));
+    const int kps_stages = (stages + splits - 1) / splits;
+    g.k_per_split = std::max(1, kps_stages) * T::BK;
+    splits = std::max(1, (g.K + g.k_per_split - 1) / g.k_per_split);
+    g.partial = nullptr;
+    if (splits > 1) {
+        CAMEL_RETURN_IF(
+            ensure_partial((size_t)splits * ntiles * T::BM * T::BN * sizeof(float)));
+        g.partial = g_partial;
+    }
+    hipLaunchKernelGGL((sgemm_kernel<T, AMODE, BMODE>), dim3((unsigned)ntiles, (unsigned)splits),
+                       dim3(T::THREADS), 0, stream(), g);
+    CAMEL_RETURN_IF(check_launch(name));
+    if (splits > 1) {
+        const size_t total = (size_t)ntiles * T::BM * T::BN;
+        hipLaunchKernelGGL((tile_reduce_kernel<T::BM, T::BN, is_conv<BMODE>>),
+                           dim3(grid_for((int64_t)total, 256)), dim3(256), 0, stream(), g, ntiles,
+                           splits);
+        CAMEL_RETURN_IF(check_launch("tile_reduce_kernel"));
+    }
+    return CAMEL_HIP_OK;
+}
+
+// Schedules all tiles.  `splits` > 1 splits every tile (small problems).
+// Otherwise whole rounds of resident work-groups run as whole tiles, and the
+// tiles of a last, partial round are split along K across the chip instead
+// of leaving most CUs idle for a whole tile time.
+template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, const char *name) {
+    const int tiles = (int)(((int64_t)(g.M + T::BM - 1) / T::BM) * ((g.N + T::BN - 1) / T::BN));
+    if (splits > 1) return launch_range<T, AMODE, BMODE>(g, 0, tiles, splits, name);
+    const int slots = resident_slots<T, AMODE, BMODE>();
+    const int stages = (g.K + T::BK - 1) / T::BK;
+    const int full = tiles / slots, rem = tiles % slots;
+    if (full == 0 || rem == 0 || stages < 4)
+        return launch_range<T, AMODE, BMODE>(g, 0, tiles, 1, name);
+    const int dp = full * slots;
+    CAMEL_RETURN_IF((launch_range<T, AMODE, BMODE>(g, 0, dp, 1, name)));
+    const int tail_splits = std::max(1, std::min(slots / rem, stages / 2));
+    return launch_range<T, AMODE, BMODE>(g, dp, rem, tail_splits, name);
+}
+
+template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool bvec) {
+    if (avec && bvec) return run_gemm<T, LOAD_VEC, LOAD_VEC>(g, splits, "sgemm_kernel");
+    if (avec) return run_gemm<T, LOAD_VEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
+    if (bvec) return run_gemm<T, LOAD_SCALAR, LOAD_VEC>(g, splits, "sgemm_kernel");
+    return run_gemm<T, LOAD_SCALAR, LOAD_SCALAR>(g, splits, "sgemm_kernel");
 }
 
 enum class Cfg { Big, Mid, Small, Skinny };
@@ -650,8 +883,7 @@ int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int
     if (rc == CAMEL_HIP_OK) {
         GemmArgs g = conv_args(static_cast<const float *>(wt), static_cast<const float *>(xt), bias,
                                y, N, C, H, W, Co, KH, KW, stride, pad, OH, OW, flags);
-        g.k_per_split = g.K;
-        rc = launch<T, LOAD_VEC, LOAD_NHWC>(g, 1, "conv2d_nhwc_kernel");
+        rc = run_gemm<T, LOAD_VEC, LOAD_NHWC>(g, 1, "conv2d_nhwc_kernel");
     }
     camel_hip_free(wt);
     camel_hip_free(xt);
@@ -698,15 +930,12 @@ int conv2d_gather(const float *x, const float *w, const float *bias, float *y, i
     g.ktab = dev_tab;
     const bool avec = (K % 4 == 0) && ((uintptr_t)w % 16 == 0);
     int rc;
-    if (Co <= 64) {
-        g.k_per_split = (int)((K + TileGather64::BK - 1) / TileGather64::BK * TileGather64::BK);
-        rc = avec ? launch<TileGather64, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
-                  : launch<TileGather64, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
-    } else {
-        g.k_per_split = (int)((K + TileGather::BK - 1) / TileGather::BK * TileGather::BK);
-        rc = avec ? launch<TileGather, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
-                  : launch<TileGather, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
-    }
+    if (Co <= 64)
+        rc = avec ? run_gemm<TileGather64, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
+                  : run_gemm<TileGather64, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
+    else
+        rc = avec ? run_gemm<TileGather, LOAD_VEC, LOAD_CONV>(g, 1, "conv2d_igemm_kernel")
+                  : run_gemm<TileGather, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
     CAMEL_RETURN_IF(rc);
     return ok();
 }
@@ -740,20 +969,15 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
     g.ldb = (int)N;
     g.ldc = (int)N;
     g.flags = flags;
+    if (thin_eligible(M, N, K)) {
+        CAMEL_RETURN_IF(launch_thin(A, B, C, (int)M, (int)N, (int)K, bias, flags));
+        return ok();
+    }
     const bool avec = (K % 4 == 0) && ((uintptr_t)A % 16 == 0);
     const bool bvec = (N % 4 == 0) && ((uintptr_t)B % 16 == 0);
     Cfg cfg;
     int splits, bk;
     choose(M, N, K, device_cu_count(), cfg, splits, bk);
-    int64_t kps = (K + splits - 1) / splits;
-    kps = (kps + bk - 1) / bk * bk;
-    if (kps == 0) kps = bk;
-    splits = (int)std::max<int64_t>(1, (K + kps - 1) / kps);
-    g.k_per_split = (int)kps;
-    if (splits > 1) {
-        CAMEL_RETURN_IF(ensure_partial((size_t)splits * M * N * sizeof(float)));
-        g.partial = g_partial;
-    }
     int rc;
     switch (cfg) {
     case Cfg::Big:
@@ -770,11 +994,6 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
         break;
     }
     CAMEL_RETURN_IF(rc);
-    if (splits > 1) {
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(M * N, 256)), dim3(256), 0,
-                           stream(), g_partial, splits, C, (int)M, (int)N, (int)N, bias, flags);
-        CAMEL_RETURN_IF(check_launch("splitk_reduce_kernel"));
-    }
     return ok();
 }
 

@@ -51,6 +51,20 @@ def test_sgemm_zero_k_gives_zeros():
     assert np.array_equal(out, O.matmul(a, b))
 
 
+@pytest.mark.parametrize("M,N,Kd", [(1024, 10, 1024), (300, 3, 50), (257, 31, 200), (100, 4, 0),
+                                    (4096, 1, 1000), (2000, 32, 512), (600, 20, 300)])
+def test_thin_n_dense_matches_oracle(M, N, Kd):
+    # N <= 32 with B small enough for LDS: the thin (non-MFMA) kernel.
+    a, w = _ab(M, N, Kd, 0x3000 + M + N + Kd)
+    b = D.uniform(0x3100 + N, (N,), -1.0, 1.0)
+    got = K.sgemm(a, w, b, H.EPI_BIAS | H.EPI_RELU)
+    ref = O.dense(a, w, b, True)
+    ok, worst = K.gemm_tol_ok(got, ref, a, w)
+    assert ok, f"worst error / bound = {worst}"
+    neg = (ref < 0) | ((ref == 0) & np.signbit(ref))
+    assert np.all(np.signbit(got[(got == 0) & neg]))
+
+
 @pytest.mark.parametrize("M,N,Kd", [(1024, 1024, 784), (1024, 1024, 1024), (512, 128, 9216)])
 def test_dense_bias_relu_matches_oracle(M, N, Kd):
     a, w = _ab(M, N, Kd, 0x2000 + Kd)
@@ -76,6 +90,20 @@ def test_square_gemm_row_slab(n):
     ref_tail = O.matmul_rows(a, b, n - 8, n)
     ok, worst = K.gemm_tol_ok(got[n - 8:], ref_tail, a[n - 8:], b)
     assert ok, f"tail worst error / bound = {worst}"
+
+
+def test_partial_round_is_split_along_k():
+    # 4352^2 in 256x256 tiles = 289 tiles on 256 resident work-groups: one
+    # whole round, then 33 tiles split along K and folded by the reduce kernel.
+    # The last tile-row and the right column band are such tail tiles.
+    n, k = 4352, 512
+    a, b = _ab(n, n, k, D.SEED_GEMM + 7)
+    bias = D.uniform(D.SEED_GEMM + 8, (n,), -1.0, 1.0)
+    got = K.sgemm(a, b, bias, H.EPI_BIAS | H.EPI_RELU)
+    for r0, r1 in ((0, 8), (3100, 3106), (n - 12, n)):
+        ref = O.dense(a[r0:r1], b, bias, True)
+        ok, worst = K.gemm_tol_ok(got[r0:r1], ref, a[r0:r1], b)
+        assert ok, f"rows {r0}-{r1}: worst error / bound = {worst}"
 
 
 def test_skinny_gemm_matches_oracle():
