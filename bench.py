@@ -9,7 +9,9 @@ elementwise and softmax bandwidth), each with its own roofline entry.
 
 Timing: W warmup steps, device sync, then exactly K steps between two HIP
 events on the library stream (the stream every kernel is launched on),
-device sync after.  `roofline.achieved` = algorithmic FLOP (or bytes) of the
+device sync after.  Suite entries warm up for at least 50 ms (the GPU clock
+ramps after idle time) and time at least 10 ms of work (microsecond kernels
+would otherwise measure host launch jitter); the CPU baseline runs last.  `roofline.achieved` = algorithmic FLOP (or bytes) of the
 dominant kernel per launch / its average launch time from those events.
 
 The CPU baseline times the oracle (a loop-for-loop restatement of the
@@ -59,10 +61,28 @@ def _progress(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# Suite entries (not the headline, which runs exactly --warmup / --steps) warm
+# up for at least this long, so the GPU clock has ramped after idle host work,
+# and time at least this much GPU work, so launches of microsecond kernels do
+# not measure host issue jitter.
+SUITE_MIN_WARM_S = 0.05
+SUITE_MIN_TIMED_S = 0.01
+_suite_mode = False
+
+
 def _time_loop(fn, steps: int, warmup: int):
-    for _ in range(warmup):
+    adaptive = _suite_mode
+    t0 = time.perf_counter()
+    n_warm = 0
+    while n_warm < warmup or (adaptive and time.perf_counter() - t0 < SUITE_MIN_WARM_S):
         fn()
+        n_warm += 1
+        if adaptive and n_warm % 8 == 0:
+            H.sync()
     H.sync()
+    if adaptive:
+        per_step = (time.perf_counter() - t0) / max(1, n_warm)
+        steps = max(steps, int(SUITE_MIN_TIMED_S / max(per_step, 1e-6)) + 1)
     t = H.Timer()
     wall0 = time.perf_counter()
     t.begin()
@@ -317,12 +337,9 @@ def main() -> int:
                    "K": 4096, "layout": "row-major contiguous", "parallelism": "single GPU"},
         "roofline": roofline_mfma(g["flop"], g["ms"], _traffic("sgemm_4096")),
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_gemm(g["a"], g["b"])
-        _progress(f"cpu baseline: {line['cpu_baseline']['value']} GFLOP/s")
-    del g
-
     if not args.no_suite:
+        global _suite_mode
+        _suite_mode = True
         suite = {}
         s_steps, s_warm = max(5, steps // 5), 2
         for n in (1024, 2048, 8192):
@@ -360,6 +377,13 @@ def main() -> int:
         line["suite"] = suite
         for k, v in suite.items():
             _progress(f"{k}: {v['value']} {v['unit']} ({100 * v['roofline']['frac']:.1f}% of peak)")
+
+    # Last, so the host-only baseline does not leave the GPU idle (and its
+    # clock low) before the suite.
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_gemm(g["a"], g["b"])
+        _progress(f"cpu baseline: {line['cpu_baseline']['value']} GFLOP/s")
+    del g
 
     print(json.dumps(line), flush=True)
     return 0

@@ -42,9 +42,15 @@ enum { LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3 };
 
 template <int M> constexpr bool is_conv = (M == LOAD_CONV || M == LOAD_NHWC);
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_> struct Tile {
-    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
-    static constexpr int THREADS = 64 * WM * WN;
+// WK > 1 splits each stage's K range over WK groups of WM x WN waves (more
+// waves per CU to hide latency when there are few tiles); the groups' sums
+// meet in LDS at the end, added in group order.  EARLY selects the stage
+// schedule with the barrier before the last 8-k group (see the main loop).
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int WK_ = 1, bool EARLY_ = true>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, WK = WK_;
+    static constexpr bool EARLY = EARLY_;
+    static constexpr int THREADS = 64 * WM * WN * WK;
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int FM = WTM / 32, FN = WTN / 32;
     static constexpr int KQ = BK / 4;
@@ -53,12 +59,18 @@ template <int BM_, int BN_, int BK_, int WM_, int WN_> struct Tile {
     static constexpr int A_STAGE = KQ * A_PLANE;
     static constexpr int B_STAGE = KQ * B_PLANE;
     static constexpr int STAGE = A_STAGE + B_STAGE;
-    static constexpr int A_ITEMS = BM * KQ / THREADS;
-    static constexpr int B_ITEMS = KQ * (BN / 4) / THREADS;
-    static constexpr int BN_ITEMS = BN * KQ / THREADS; // B as pixel rows (LOAD_NHWC)
+    // 16-byte load items per stage; a thread takes items tid + i * THREADS.
+    static constexpr int A_TOTAL = BM * KQ;
+    static constexpr int B_TOTAL = KQ * (BN / 4);
+    static constexpr int BN_TOTAL = BN * KQ; // B as pixel rows (LOAD_NHWC)
+    static constexpr int A_ITEMS = (A_TOTAL + THREADS - 1) / THREADS;
+    static constexpr int B_ITEMS = (B_TOTAL + THREADS - 1) / THREADS;
+    static constexpr int BN_ITEMS = (BN_TOTAL + THREADS - 1) / THREADS;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
-    static_assert(BK % 8 == 0, "BK must be a multiple of 8");
-    static_assert((BM * KQ) % THREADS == 0, "A stage must split evenly over threads");
+    static_assert(BN % 32 == 0, "B column swizzle works on aligned runs of 32 columns");
+    static_assert(BK % (8 * WK) == 0, "each wave k-group takes whole 8-k groups of a stage");
+    static_assert(A_TOTAL % 64 == 0 && B_TOTAL % 64 == 0, "item guards must be wave-uniform");
+    static_assert((WK - 1) * BM * BN <= 2 * STAGE, "k-group reduction must fit the LDS buffers");
 };
 
 struct GemmArgs {
@@ -77,6 +89,13 @@ struct GemmArgs {
     int P, OW, H, W, CHW, stride, pad;
     int Cin, KW;
 };
+
+// LDS slot of B column n within a k-quad plane.  A 16-byte LDS access is
+// served 8 lanes at a time over the 32 banks; the register-transposed B
+// stores have lanes 4 columns apart (n = 4 nq + c), which would put 8 lanes
+// on 2 bank groups.  XOR-ing bits 0-1 with bits 3-4 spreads them over all 8,
+// and keeps each aligned run of 8 columns (one 8-lane operand read) whole.
+__device__ __forceinline__ int b_slot(int n) { return n ^ ((n >> 3) & 3); }
 
 // Logical tile id -> (tm, tn), grouped GROUP_M tile-rows deep so that
 // consecutive ids share B panels.  A bijection on [0, tiles_m * tiles_n).
@@ -118,10 +137,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     if constexpr (BMODE == LOAD_NHWC) {
         static_assert((T::BN * T::KQ) % T::THREADS == 0, "B pixel rows must split evenly");
     } else {
-        static_assert((T::KQ * (T::BN / 4)) % T::THREADS == 0, "B stage must split evenly");
         static_assert(T::THREADS % (T::BN / 4) == 0 || (T::BN / 4) % T::THREADS == 0,
                       "B column mapping");
     }
+    // Items past a stage's count (when THREADS does not divide it) are skipped
+    // by whole waves.
+    constexpr bool A_TAIL = T::A_TOTAL % T::THREADS != 0;
+    constexpr bool B_TAIL = T::B_TOTAL % T::THREADS != 0;
     // One stage of operands in flight from global memory to LDS.
     struct StageRegs {
         float4 ra[T::A_ITEMS];
@@ -189,6 +211,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < T::A_ITEMS; ++i) {
             const int q = tid + i * T::THREADS;
+            if (A_TAIL && q >= T::A_TOTAL) break;
             const int kq = q % T::KQ, m = q / T::KQ;
             const int gm = m0 + m, gk = k0 + 4 * kq;
             const float *src = g.A + (size_t)gm * g.lda + gk;
@@ -222,6 +245,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < (BMODE == LOAD_NHWC ? 0 : T::B_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
+            if (B_TAIL && q >= T::B_TOTAL) break;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
             if constexpr (BMODE == LOAD_VEC) {
                 const int gn = n0 + 4 * nq;
@@ -273,6 +297,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < T::A_ITEMS; ++i) {
             const int q = tid + i * T::THREADS;
+            if (A_TAIL && q >= T::A_TOTAL) break;
             const int kq = q % T::KQ, m = q / T::KQ;
             *reinterpret_cast<float4 *>(As + kq * T::A_PLANE + m * 4) = ra[i];
         }
@@ -281,12 +306,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             for (int i = 0; i < T::BN_ITEMS; ++i) {
                 const int q = tid + i * T::THREADS;
                 const int kq = q % T::KQ, n = q / T::KQ;
-                *reinterpret_cast<float4 *>(Bs + kq * T::B_PLANE + n * 4) = rbn[i];
+                *reinterpret_cast<float4 *>(Bs + kq * T::B_PLANE + b_slot(n) * 4) = rbn[i];
             }
         }
 #pragma unroll
         for (int i = 0; i < (BMODE == LOAD_NHWC ? 0 : T::B_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
+            if (B_TAIL && q >= T::B_TOTAL) break;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
             float *plane = Bs + kq * T::B_PLANE;
             // rb[i][u] holds row k0+4kq+u for 4 columns; LDS wants, per column,
@@ -299,14 +325,15 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 col.y = rb[i][1][c];
                 col.z = rb[i][2][c];
                 col.w = rb[i][3][c];
-                *reinterpret_cast<float4 *>(plane + n * 4) = col;
+                *reinterpret_cast<float4 *>(plane + b_slot(n) * 4) = col;
             }
         }
     };
 
     const int wave = tid >> 6, lane = tid & 63;
     const int half = lane >> 5, r32 = lane & 31;
-    const int wm = wave / T::WN, wn = wave % T::WN;
+    const int wk = wave / (T::WM * T::WN), wsp = wave % (T::WM * T::WN);
+    const int wm = wsp / T::WN, wn = wsp % T::WN;
 
     floatx16 acc[T::FM][T::FN];
 #pragma unroll
@@ -316,59 +343,101 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    // LDS operand reads run one 8-k group ahead of the MFMAs that use them, so
-    // each group's ds_read latency hides behind the previous group's MFMAs.
-    auto compute_stage = [&](int kt) {
+    // Schedule of one stage kt (G = 8-k groups per wave):
+    //   * the global loads of stage kt+1 are issued first (registers);
+    //   * LDS operand reads run one 8-k group ahead of the MFMAs that use them,
+    //     so each group's ds_read latency hides behind the previous group's
+    //     MFMAs;
+    //   * EARLY: halfway through, stage kt+1 is stored to the other LDS buffer
+    //     (its last readers finished before the previous barrier), and the
+    //     barrier comes before the last group's MFMAs, with the first reads of
+    //     stage kt+1 issued right after it, so those MFMAs cover the read
+    //     latency and the barrier costs little more than the waves' skew
+    //     (measured faster for 64x64 and 128x128 tiles);
+    //   * otherwise: all G groups, then the store and the barrier (measured
+    //     faster for the 8-wave 256x256 tile, whose long stages already hide
+    //     the barrier).
+    constexpr int GROUPS = T::BK / 8 / T::WK; // 8-k groups of this wave's k-group
+    constexpr int STORE_AT = GROUPS / 2 - 1;   // store after this group's MFMAs
+    static_assert(GROUPS % 2 == 0, "operand registers alternate between even and odd groups");
+    auto operand_bases = [&](int kt, const float *&a_base, const float *&b_base) {
         const float *As = smem + (kt & 1) * T::STAGE;
         const float *Bs = As + T::A_STAGE;
-        const float *a_base = As + half * T::A_PLANE + (wm * T::WTM + r32) * 4;
-        const float *b_base = Bs + half * T::B_PLANE + (wn * T::WTN + r32) * 4;
-        constexpr int GROUPS = T::BK / 8;
-        float4 a[2][T::FM], b[2][T::FN];
-        auto fetch = [&](int s8, float4 *fa, float4 *fb) {
+        a_base = As + (2 * GROUPS * wk + half) * T::A_PLANE + (wm * T::WTM + r32) * 4;
+        b_base = Bs + (2 * GROUPS * wk + half) * T::B_PLANE + (wn * T::WTN + b_slot(r32)) * 4;
+    };
+    auto fetch = [&](const float *a_base, const float *b_base, int s8, float4 *fa, float4 *fb) {
+#pragma unroll
+        for (int i = 0; i < T::FM; ++i)
+            fa[i] = *reinterpret_cast<const float4 *>(a_base + 2 * s8 * T::A_PLANE + i * 128);
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j)
+            fb[j] = *reinterpret_cast<const float4 *>(b_base + 2 * s8 * T::B_PLANE + j * 128);
+    };
+    auto mfma_group = [&](const float4 *fa, const float4 *fb) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int i = 0; i < T::FM; ++i)
-                fa[i] = *reinterpret_cast<const float4 *>(a_base + 2 * s8 * T::A_PLANE + i * 128);
 #pragma unroll
-            for (int j = 0; j < T::FN; ++j)
-                fb[j] = *reinterpret_cast<const float4 *>(b_base + 2 * s8 * T::B_PLANE + j * 128);
-        };
-        fetch(0, a[0], b[0]);
-        __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
-#pragma unroll
-        for (int s8 = 0; s8 < GROUPS; ++s8) {
-            const int cur = s8 & 1;
-            if (s8 + 1 < GROUPS) fetch(s8 + 1, a[cur ^ 1], b[cur ^ 1]);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int i = 0; i < T::FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < T::FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][i][t], b[cur][j][t],
-                                                                          acc[i][j], 0, 0, 0);
-            // Keep the order above: the next group's LDS reads issue before
-            // this group's MFMAs (masks: 0x100 LDS read, 0x8 MFMA).
-            if (s8 + 1 < GROUPS) __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
-        }
+                for (int j = 0; j < T::FN; ++j)
+                    acc[i][j] =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][t], fb[j][t], acc[i][j], 0, 0, 0);
     };
     auto lds_stage = [&](int kt) { return smem + (kt & 1) * T::STAGE; };
 
-    // Stage kt+1 is fetched into registers while stage kt is multiplied, then
-    // stored to the other LDS buffer; one barrier per stage.
     auto main_loop = [&](auto full_tag) {
-        if (nk > 0) {
-            load_stage(full_tag, kbeg, R0);
-            store_stage(smem, smem + T::A_STAGE, R0);
-            __syncthreads();
+        if (nk <= 0) return;
+        load_stage(full_tag, kbeg, R0);
+        store_stage(smem, smem + T::A_STAGE, R0);
+        __syncthreads();
+        float4 fa[2][T::FM], fb[2][T::FN];
+        const float *a_base, *b_base;
+        if constexpr (!T::EARLY) {
+            for (int kt = 0; kt < nk; ++kt) {
+                const bool more = kt + 1 < nk;
+                if (more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0);
+                operand_bases(kt, a_base, b_base);
+                fetch(a_base, b_base, 0, fa[0], fb[0]);
+                __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
+#pragma unroll
+                for (int s8 = 0; s8 < GROUPS; ++s8) {
+                    const int cur = s8 & 1;
+                    if (s8 + 1 < GROUPS) fetch(a_base, b_base, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                    if (s8 + 1 < GROUPS) __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
+                    mfma_group(fa[cur], fb[cur]);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
+                }
+                if (more) store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
+                __syncthreads();
+            }
+            return;
         }
+        operand_bases(0, a_base, b_base);
+        fetch(a_base, b_base, 0, fa[0], fb[0]);
         for (int kt = 0; kt < nk; ++kt) {
             const bool more = kt + 1 < nk;
             if (more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0);
-            compute_stage(kt);
-            if (more) store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
+#pragma unroll
+            for (int s8 = 0; s8 + 1 < GROUPS; ++s8) {
+                const int cur = s8 & 1;
+                fetch(a_base, b_base, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                // Keep the order: the next group's LDS reads issue before this
+                // group's MFMAs (masks: 0x100 LDS read, 0x8 MFMA).
+                __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
+                mfma_group(fa[cur], fb[cur]);
+                __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
+                if (s8 == STORE_AT && more)
+                    store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
+            }
             __syncthreads();
+            if (more) {
+                operand_bases(kt + 1, a_base, b_base);
+                fetch(a_base, b_base, 0, fa[0], fb[0]);
+                __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
+            }
+            mfma_group(fa[1], fb[1]);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
         }
     };
     const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N) &&
@@ -377,6 +446,43 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         main_loop(std::true_type{});
     else
         main_loop(std::false_type{});
+
+    if constexpr (T::WK > 1) {
+        // k-groups 1..WK-1 hand their sums to group 0 through LDS (free after
+        // the loop's last barrier); group 0 adds them in group order.
+        constexpr int PER_LANE = T::FM * T::FN * 4; // float4 per lane
+        float4 *red = reinterpret_cast<float4 *>(smem);
+        auto slot = [&](int grp, int i, int j, int q) {
+            return ((((grp - 1) * T::WM * T::WN + wsp) * PER_LANE + (i * T::FN + j) * 4 + q) << 6) +
+                   lane;
+        };
+        if (wk > 0) {
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::FN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        red[slot(wk, i, j, q)] = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                             acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+        }
+        __syncthreads();
+        if (wk > 0) return;
+        for (int grp = 1; grp < T::WK; ++grp) {
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+                for (int j = 0; j < T::FN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 v = red[slot(grp, i, j, q)];
+                        acc[i][j][4 * q + 0] += v.x;
+                        acc[i][j][4 * q + 1] += v.y;
+                        acc[i][j][4 * q + 2] += v.z;
+                        acc[i][j][4 * q + 3] += v.w;
+                    }
+        }
+    }
 
     // ---- epilogue ----
     const bool has_bias = (g.flags & CAMEL_EPI_BIAS) != 0 && g.partial == nullptr;
@@ -559,6 +665,168 @@ int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, c
     return go(sgemm_thin_kernel<32, 2>);
 }
 
+// Skinny GEMM (M <= 32, e.g. M = 16, N = K = 4096): B is read once from HBM
+// and dominates the traffic, so the kernel is a streaming pass over B.
+//   * a work-group owns 64 columns x SK_KB k, its 8 waves SK_KB / 8 k each;
+//     per 4-k step lane l loads one 16-byte chunk of B row k0 + 4s + l/16,
+//     columns n0 + 4 (l % 16) .. +3, so 16 lanes cover 256 contiguous bytes
+//     of a row; the wave's B loads are all issued before A is staged;
+//   * v_mfma_f32_16x16x4_f32 takes A[i][k] from lane i + 16 k and B[k][j]
+//     from lane j + 16 k; the 4 floats of a lane's chunk feed 4 MFMAs whose
+//     column j stands for column n0 + 4 j + c (c = 0..3), so no shuffle is
+//     needed; the accumulator of MFMA c holds rows 4 (l / 16) + v at column
+//     n0 + 4 (l % 16) + c;
+//   * the work-group's A panel (rows x SK_KB) is staged in LDS with
+//     coalesced loads (per-lane A loads of 16 rows x 4 k cost more);
+//   * the 8 waves' sums meet in LDS in wave order; work-groups along K
+//     (blockIdx.y) write partials [ks][M][N] that skinny_reduce_kernel sums
+//     in ks order before the epilogue (letting the last work-group of a
+//     strip do it needs device-scope fences, and each one writes back and
+//     invalidates the XCD's L2: measured several times slower).
+constexpr int SK_WAVES = 8;
+constexpr int SK_COLS = 64;
+constexpr int SK_STEPS = 8;                     // 4-k steps per wave
+constexpr int SK_KB = SK_WAVES * 4 * SK_STEPS;  // k per work-group
+
+template <int MT>
+__global__ __launch_bounds__(SK_WAVES * 64) void sgemm_skinny_kernel(
+    const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N,
+    int K, const float *__restrict__ bias, int flags, float *__restrict__ partial) {
+    typedef float floatx4 __attribute__((ext_vector_type(4)));
+    constexpr int STEPS = SK_STEPS, KW = 4 * STEPS, KB = SK_KB;
+    constexpr int AS = KB + 4; // LDS row stride of the A panel
+    __shared__ __attribute__((aligned(16))) float as[16 * MT * AS];
+    __shared__ float4 red[SK_WAVES][MT * 4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, q = lane >> 4;
+    const int strip = blockIdx.x, ks = blockIdx.y, nks = gridDim.y;
+    const int n0 = strip * SK_COLS;
+    const int kb0 = ks * KB;
+    const int k0 = kb0 + wave * KW + q;
+    const int col = n0 + 4 * r16;
+    const bool col_ok = col < N; // N % 4 == 0: a chunk is all in or all out
+
+    // FULL (every row, column and k in range, the common case) has no
+    // guards: a guarded load compiles to a branch, after which the compiler
+    // waits for all loads at once instead of one by one.
+    float4 b[STEPS];
+    auto load_b = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const int k = k0 + 4 * s;
+            b[s] = (FULL || (col_ok && k < K))
+                       ? *reinterpret_cast<const float4 *>(B + (size_t)k * N + col)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    const bool full = n0 + SK_COLS <= N && kb0 + KB <= K;
+    if (full)
+        load_b(std::true_type{});
+    else
+        load_b(std::false_type{});
+    if (full && M >= 16 * MT && (K & 3) == 0 && ((uintptr_t)A & 15) == 0) {
+        // 16-byte chunks, no guards
+#pragma unroll
+        for (int i = threadIdx.x; i < 16 * MT * KB / 4; i += SK_WAVES * 64) {
+            const int m = i / (KB / 4), kk = 4 * (i - m * (KB / 4));
+            *reinterpret_cast<float4 *>(as + m * AS + kk) =
+                *reinterpret_cast<const float4 *>(A + (size_t)m * K + kb0 + kk);
+        }
+    } else {
+        for (int i = threadIdx.x; i < 16 * MT * KB; i += SK_WAVES * 64) {
+            const int m = i / KB, kk = i - m * KB, k = kb0 + kk;
+            as[m * AS + kk] = (m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
+        }
+    }
+    __syncthreads();
+    float a[MT][STEPS];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) a[t][s] = as[(16 * t + r16) * AS + wave * KW + q + 4 * s];
+    floatx4 acc[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[t][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].x, acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].y, acc[t][1], 0, 0, 0);
+            acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].z, acc[t][2], 0, 0, 0);
+            acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].w, acc[t][3], 0, 0, 0);
+        }
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            red[wave][t * 4 + c][lane] = make_float4(acc[t][c][0], acc[t][c][1], acc[t][c][2],
+                                                     acc[t][c][3]);
+    __syncthreads();
+
+    // Thread x < MT*4*64 owns accumulator slot (t, c) of lane x % 64: rows
+    // 16 t + 4 (l / 16) + v, column n0 + 4 (l % 16) + c.
+    const int x = threadIdx.x;
+    const bool owner = x < MT * 4 * 64;
+    const int slot = x >> 6, sl = x & 63;
+    const int t = slot >> 2, c = slot & 3;
+    const int row0 = 16 * t + 4 * (sl >> 4), ocol = n0 + 4 * (sl & 15) + c;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (owner) {
+#pragma unroll
+        for (int w = 0; w < SK_WAVES; ++w) {
+            const float4 p = red[w][slot][sl];
+            v[0] += p.x;
+            v[1] += p.y;
+            v[2] += p.z;
+            v[3] += p.w;
+        }
+    }
+    auto finish = [&](const float *vals) {
+        if (!owner || ocol >= N) return;
+        const float bcol = (flags & CAMEL_EPI_BIAS) ? bias[ocol] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + i;
+            if (row >= M) continue;
+            float y = vals[i];
+            if (flags & CAMEL_EPI_BIAS) y = y + bcol;
+            if (flags & CAMEL_EPI_RELU) y = relu_idiom(y);
+            C[(size_t)row * N + ocol] = y;
+        }
+    };
+    if (nks == 1) {
+        finish(v);
+        return;
+    }
+    // partial layout [ks][M][N]
+    if (owner && ocol < N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + i;
+            if (row < M) partial[((size_t)ks * M + row) * N + ocol] = v[i];
+        }
+    }
+}
+
+// Sums the skinny kernel's k partials in ks order, then bias and relu.
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float *__restrict__ partial,
+                                                            float *__restrict__ C, int M, int N,
+                                                            int nks, const float *__restrict__ bias,
+                                                            int flags) {
+    const size_t total = (size_t)M * N;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    float y = partial[idx];
+    for (int z = 1; z < nks; ++z) y = y + partial[(size_t)z * total + idx];
+    if (flags & CAMEL_EPI_BIAS) y = y + bias[idx % N];
+    if (flags & CAMEL_EPI_RELU) y = relu_idiom(y);
+    C[idx] = y;
+}
+
 // Mixed-dtype matmul: one thread per output, double accumulation in k order
 // exactly as operators.cpp:757-766, rounded through setFromDouble.
 __global__ void matmul_generic_kernel(int adt, const void *A, int bdt, const void *B, int odt,
@@ -676,9 +944,9 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
 // BASELINE conv shapes): 8 waves at 256x256 keep the accumulators in arch
 // VGPRs without spills; the conv tiles are small enough for two work-groups
 // per CU, which hides the gather latency better than larger tiles do.
-using TileBig = Tile<256, 256, 32, 2, 4>;    // wave 128x64, 8 waves
-using TileMid = Tile<128, 128, 32, 2, 2>;    // wave 64x64
-using TileSmall = Tile<64, 64, 64, 2, 2>;    // wave 32x32
+using TileBig = Tile<256, 256, 32, 2, 4, 1, false>; // wave 128x64, 8 waves
+using TileMid = Tile<128, 128, 32, 2, 2>;           // wave 64x64
+using TileSmall = Tile<64, 64, 64, 2, 2, 2>;        // wave 32x32, two k-groups (8 waves)
 using TileSkinny = Tile<32, 128, 64, 1, 4>;  // wave 32x32, M <= 32
 using TileConv = Tile<128, 128, 32, 2, 2>;   // NHWC conv, Co > 64, C % 32 == 0
 using TileConv16 = Tile<128, 128, 16, 2, 2>; // NHWC conv, Co > 64, C % 16 == 0
@@ -708,6 +976,29 @@ int ensure_partial(size_t bytes) {
     g_partial = static_cast<float *>(p);
     g_partial_bytes = bytes;
     return CAMEL_HIP_OK;
+}
+
+// True when the streaming skinny kernel serves C[M, N] = A[M, K] B[K, N].
+bool skinny_eligible(int64_t M, int64_t N, int64_t K, const float *B) {
+    return M <= 32 && K > 0 && N % 4 == 0 && ((uintptr_t)B & 15) == 0;
+}
+
+int launch_skinny(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
+                  int flags) {
+    const int strips = (N + SK_COLS - 1) / SK_COLS;
+    auto go = [&](auto kernel) -> int {
+        const int nks = (K + SK_KB - 1) / SK_KB;
+        if (nks > 1) CAMEL_RETURN_IF(ensure_partial((size_t)nks * M * N * sizeof(float)));
+        hipLaunchKernelGGL(kernel, dim3((unsigned)strips, (unsigned)nks), dim3(SK_WAVES * 64), 0,
+                           stream(), A, B, C, M, N, K, bias, flags, g_partial);
+        CAMEL_RETURN_IF(check_launch("sgemm_skinny_kernel"));
+        if (nks == 1) return CAMEL_HIP_OK;
+        const int64_t total = (int64_t)M * N;
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                           stream(), g_partial, C, M, N, nks, bias, flags);
+        return check_launch("skinny_reduce_kernel");
+    };
+    return M <= 16 ? go(sgemm_skinny_kernel<1>) : go(sgemm_skinny_kernel<2>);
 }
 
 // Work-groups of one kernel that fit on the chip at once (occupancy x CUs).
@@ -795,9 +1086,6 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
     } else if (tiles_of<TileMid>(M, N) >= cus) {
         cfg = Cfg::Mid;
         bk = TileMid::BK;
-        // One tile per CU leaves the MFMA pipes half fed; a 2-way K split of
-        // long reductions measured 8% faster at 2048^3.
-        if (tiles_of<TileMid>(M, N) < 2 * cus && K >= 2048) splits = 2;
         return;
     } else {
         cfg = Cfg::Small;
@@ -971,6 +1259,10 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
     g.flags = flags;
     if (thin_eligible(M, N, K)) {
         CAMEL_RETURN_IF(launch_thin(A, B, C, (int)M, (int)N, (int)K, bias, flags));
+        return ok();
+    }
+    if (skinny_eligible(M, N, K, B)) {
+        CAMEL_RETURN_IF(launch_skinny(A, B, C, (int)M, (int)N, (int)K, bias, flags));
         return ok();
     }
     const bool avec = (K % 4 == 0) && ((uintptr_t)A % 16 == 0);

@@ -114,6 +114,35 @@ def test_skinny_gemm_matches_oracle():
     assert ok, f"worst error / bound = {worst}"
 
 
+@pytest.mark.parametrize("M,N,Kd", [
+    (16, 4096, 1000),   # K tail inside one wave's range
+    (32, 4100, 3000),   # two 16-row groups, last strip partial, short k ranges
+    (17, 64, 5000),     # one strip, many k work-groups
+    (3, 8, 7),          # one work-group, no partials
+    (16, 256, 65536),   # 64 k work-groups per strip
+])
+def test_skinny_streaming_kernel_matches_oracle(M, N, Kd):
+    # M <= 32, N % 4 == 0: the streaming kernel (16x16x4 MFMA), k partials
+    # summed in order by the reduce kernel, which applies bias + relu.
+    a, b = _ab(M, N, Kd, 0x4000 + M + N + Kd)
+    bias = D.uniform(0x4100 + N, (N,), -1.0, 1.0)
+    ref = O.dense(a, b, bias, True)
+    for _ in range(2):  # a second call reuses the partial scratch
+        got = K.sgemm(a, b, bias, H.EPI_BIAS | H.EPI_RELU)
+        ok, worst = K.gemm_tol_ok(got, ref, a, b)
+        assert ok, f"worst error / bound = {worst}"
+    neg = (ref < 0) | ((ref == 0) & np.signbit(ref))
+    assert np.all(np.signbit(got[(got == 0) & neg]))
+
+
+def test_skinny_results_do_not_depend_on_scheduling():
+    # The k work-groups of a strip finish in any order; the sum order is fixed.
+    a, b = _ab(16, 1024, 8192, 0x4200)
+    first = K.sgemm(a, b)
+    for _ in range(3):
+        assert np.array_equal(K.sgemm(a, b).view(np.uint32), first.view(np.uint32))
+
+
 def test_identity_and_ones_closed_forms():
     # A @ I = A exactly; ones @ ones = K exactly (tensor_smoke.cml:9-11 pattern)
     a = D.uniform(7, (300, 260), -1, 1)
