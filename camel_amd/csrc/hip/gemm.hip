@@ -878,27 +878,25 @@ __global__ void weights_khwc_kernel(const float *__restrict__ w, float *__restri
 }
 
 // Direct convolution for a tiny reduction (C*KH*KW <= DIRECT_MAX_K, e.g. the
-// first layer of an image CNN with C = 1): one thread per output pixel and
-// DIRECT_CO output channels; the weights of the block's channels sit in LDS.
-// Accumulation runs in k = (c, kh, kw) ascending order with fp32 FMA, the
-// same order as the GEMM path; bias then relu as x * (x > 0).
+// first layer of an image CNN with C = 1): one thread per output pixel, all
+// output channels.  The patch is loaded once into registers; the weights are
+// wave-uniform and come in through scalar loads, so each output channel is
+// KH*KW*C FMAs with a scalar operand, and the kernel runs at the speed of
+// its output stores.  Accumulation runs in k = (c, kh, kw) ascending order
+// with fp32 FMA, the same order as the GEMM path; bias then relu as
+// x * (x > 0).
 constexpr int DIRECT_MAX_K = 32;
-constexpr int DIRECT_CO = 8;
 
-// KMAX >= C*KH*KW: the k loops unroll over KMAX so the patch stays in registers.
-template <int KMAX>
+// KMAX >= C*KH*KW: the k loops unroll over KMAX so the patch stays in
+// registers.  EXACT (KMAX == C*KH*KW): no per-k guard, so the weight loads of
+// a channel batch into a few scalar loads (a guarded one becomes a branch
+// around a lone scalar load and its full latency).
+template <int KMAX, bool EXACT>
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(
     const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
     int stride, int pad, int flags) {
-    __shared__ float ws[DIRECT_CO * KMAX];
     const int K = C * KH * KW;
-    const int co0 = blockIdx.y * DIRECT_CO;
-    for (int i = threadIdx.x; i < DIRECT_CO * KMAX; i += blockDim.x) {
-        const int co = co0 + i / KMAX, k = i % KMAX;
-        ws[i] = (co < Co && k < K) ? w[(size_t)co * K + k] : 0.f;
-    }
-    __syncthreads();
     const int pg = blockIdx.x * blockDim.x + threadIdx.x;
     if (pg >= NP) return;
     const int img = pg / P, p = pg - img * P;
@@ -910,7 +908,7 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
 #pragma unroll
     for (int k = 0; k < KMAX; ++k) {
         float v = 0.f;
-        if (k < K) {
+        if (EXACT || k < K) {
             const int ih = ih0 + kh, iw = iw0 + kw;
             if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
                 v = xi[(size_t)c * H * W + (size_t)ih * W + iw];
@@ -924,18 +922,33 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
         }
         xv[k] = v;
     }
+    float *yo = y + (size_t)img * Co * P + p;
+    // Epilogue flags are fixed per variant so the channel loop has no
+    // branches and its scalar loads batch across unrolled channels.
+    auto channels = [&](auto has_bias, auto has_relu) {
+#pragma unroll 4
+        for (int co = 0; co < Co; ++co) {
+            const float *wr = w + (size_t)co * K;
+            float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < DIRECT_CO; ++j) {
-        const int co = co0 + j;
-        if (co >= Co) break;
-        float acc = 0.f;
-#pragma unroll
-        for (int k = 0; k < KMAX; ++k)
-            if (k < K) acc = __builtin_fmaf(ws[j * KMAX + k], xv[k], acc);
-        if (flags & CAMEL_EPI_BIAS) acc = acc + bias[co];
-        if (flags & CAMEL_EPI_RELU) acc = relu_idiom(acc);
-        y[((size_t)img * Co + co) * P + p] = acc;
-    }
+            for (int k = 0; k < KMAX; ++k)
+                if (EXACT || k < K) acc = __builtin_fmaf(wr[k], xv[k], acc);
+            if constexpr (decltype(has_bias)::value) acc = acc + bias[co];
+            if constexpr (decltype(has_relu)::value) acc = relu_idiom(acc);
+            yo[(size_t)co * P] = acc;
+        }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool b = (flags & CAMEL_EPI_BIAS) != 0, r = (flags & CAMEL_EPI_RELU) != 0;
+    if (b && r)
+        channels(T_{}, T_{});
+    else if (b)
+        channels(T_{}, F_{});
+    else if (r)
+        channels(F_{}, T_{});
+    else
+        channels(F_{}, F_{});
 }
 
 // ---- host-side launch -----------------------------------------------------------
@@ -1106,19 +1119,25 @@ int conv2d_direct(const float *x, const float *w, const float *bias, float *y, i
                   int64_t pad, int64_t OH, int64_t OW, int flags) {
     const int64_t P = OH * OW, NP = N * P;
     const int64_t K = C * KH * KW;
-    dim3 grid((unsigned)((NP + 255) / 256), (unsigned)((Co + DIRECT_CO - 1) / DIRECT_CO));
+    dim3 grid((unsigned)((NP + 255) / 256));
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream(), x, w, bias, y, (int)NP, (int)P,
                            (int)OW, (int)C, (int)H, (int)W, (int)Co, (int)KH, (int)KW, (int)stride,
                            (int)pad, flags);
         return check_launch("conv2d_direct_kernel");
     };
-    if (K <= 9)
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<9>));
+    // Exact kernels for the usual first layers: 3x3 and 5x5 over 1 or 3
+    // channels.
+    if (K == 9)
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<9, true>));
+    else if (K == 25)
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<25, true>));
+    else if (K == 27)
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<27, true>));
     else if (K <= 16)
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<16>));
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<16, false>));
     else
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<DIRECT_MAX_K>));
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<DIRECT_MAX_K, false>));
     return ok();
 }
 
