@@ -845,9 +845,25 @@ __global__ void matmul_generic_kernel(int adt, const void *A, int bdt, const voi
 // ---- conv helpers ----------------------------------------------------------------
 
 // x [N][C][HW] -> xt [N][HW][C]: 32x32 tiles through LDS, one image per z.
+// The extra z slice (z == N) reorders the weights w [Co][C][KHW] ->
+// wt [Co][KHW][C] (K ordered (kh, kw, c)) in the same launch.
 __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const float *__restrict__ x,
-                                                           float *__restrict__ xt, int C, int HW) {
+                                                           float *__restrict__ xt, int C, int HW,
+                                                           const float *__restrict__ w,
+                                                           float *__restrict__ wt, int Co,
+                                                           int KHW) {
     __shared__ float tile[32][33];
+    if (blockIdx.z == gridDim.z - 1) {
+        const int total = Co * C * KHW;
+        const int nthreads = gridDim.x * gridDim.y * blockDim.x;
+        for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+             i += nthreads) {
+            const int co = i / (C * KHW), r = i - co * C * KHW;
+            const int c = r / KHW, khw = r - c * KHW;
+            wt[(size_t)co * C * KHW + (size_t)khw * C + c] = w[i];
+        }
+        return;
+    }
     const size_t img = blockIdx.z;
     const float *src = x + img * (size_t)C * HW;
     float *dst = xt + img * (size_t)C * HW;
@@ -863,17 +879,6 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const float *__restri
     for (int k = ty; k < 32; k += 8) {
         const int p = p0 + k, c = c0 + tx;
         if (c < C && p < HW) dst[(size_t)p * C + c] = tile[tx][k];
-    }
-}
-
-// w [Co][C][KH][KW] -> wt [Co][KH][KW][C] (K ordered (kh, kw, c)).
-__global__ void weights_khwc_kernel(const float *__restrict__ w, float *__restrict__ wt, int Co,
-                                    int C, int KHW) {
-    const int total = Co * C * KHW;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
-        const int co = i / (C * KHW), r = i - co * C * KHW;
-        const int c = r / KHW, khw = r - c * KHW;
-        wt[(size_t)co * C * KHW + (size_t)khw * C + c] = w[i];
     }
 }
 
@@ -966,7 +971,7 @@ using TileConv16 = Tile<128, 128, 16, 2, 2>; // NHWC conv, Co > 64, C % 16 == 0
 using TileConv64 = Tile<64, 128, 32, 2, 2>;  // NHWC conv, Co <= 64, C % 32 == 0
 using TileConv64k16 = Tile<64, 128, 16, 2, 2>; // NHWC conv, Co <= 64, C % 16 == 0
 using TileGather = Tile<128, 256, 16, 2, 2>;   // NCHW gather conv, Co > 64
-using TileGather64 = Tile<64, 256, 32, 1, 4>;  // NCHW gather conv, Co <= 64
+using TileGather64 = Tile<64, 128, 32, 2, 2>;  // NCHW gather conv, Co <= 64 (no spills)
 
 template <class T> int64_t tiles_of(int64_t M, int64_t N) {
     return ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
@@ -1177,15 +1182,11 @@ int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int
     CAMEL_RETURN_IF(camel_hip_malloc(&xt, (size_t)(N * C * HW) * sizeof(float)));
     int rc = camel_hip_malloc(&wt, (size_t)(Co * K) * sizeof(float));
     if (rc == CAMEL_HIP_OK) {
-        dim3 tgrid((unsigned)((HW + 31) / 32), (unsigned)((C + 31) / 32), (unsigned)N);
+        dim3 tgrid((unsigned)((HW + 31) / 32), (unsigned)((C + 31) / 32), (unsigned)(N + 1));
         hipLaunchKernelGGL(nchw_to_nhwc_kernel, tgrid, dim3(256), 0, stream(), x,
-                           static_cast<float *>(xt), (int)C, (int)HW);
+                           static_cast<float *>(xt), (int)C, (int)HW, w, static_cast<float *>(wt),
+                           (int)Co, (int)(KH * KW));
         rc = check_launch("nchw_to_nhwc_kernel");
-    }
-    if (rc == CAMEL_HIP_OK) {
-        hipLaunchKernelGGL(weights_khwc_kernel, dim3(grid_for(Co * K, 256)), dim3(256), 0, stream(),
-                           w, static_cast<float *>(wt), (int)Co, (int)C, (int)(KH * KW));
-        rc = check_launch("weights_khwc_kernel");
     }
     if (rc == CAMEL_HIP_OK) {
         GemmArgs g = conv_args(static_cast<const float *>(wt), static_cast<const float *>(xt), bias,
@@ -1344,7 +1345,8 @@ int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y
     if (K <= DIRECT_MAX_K) return conv2d_direct(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
                                                 OW, flags);
     const bool aligned = (((uintptr_t)x | (uintptr_t)w) & 15) == 0;
-    if (aligned && C % 16 == 0) {
+    // The NHWC transpose runs one image per grid z (plus one z for the weights).
+    if (aligned && C % 16 == 0 && N < 65535) {
         const bool k32 = C % 32 == 0;
         if (Co > 64)
             return k32 ? conv2d_nhwc<TileConv>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
