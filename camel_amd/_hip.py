@@ -44,6 +44,7 @@ _D = C.c_double
 _SIGNATURES = {
     "camel_hip_init": [_I],
     "camel_hip_device_count": [C.POINTER(_I)],
+    "camel_hip_current_device": [C.POINTER(_I)],
     "camel_hip_last_error": [],
     "camel_hip_sync": [],
     "camel_hip_stream": [],

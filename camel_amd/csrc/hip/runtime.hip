@@ -183,6 +183,14 @@ int camel_hip_sync(void) {
     return ok();
 }
 
+int camel_hip_current_device(int *device) {
+    if (!device) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_current_device: null pointer");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    *device = state().device;
+    return ok();
+}
+
 void *camel_hip_stream(void) {
     CAMEL_LOCK();
     if (ensure_init() != CAMEL_HIP_OK) return nullptr;

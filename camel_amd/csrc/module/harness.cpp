@@ -153,6 +153,23 @@ int camel_tensor_release(uint64_t handle) {
     return ok();
 }
 
+int camel_tensor_to_dlpack(uint64_t handle, int on_device, DLManagedTensor **managed) {
+    TensorObject *t = tensorOf(handle);
+    if (!t || !managed) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_to_dlpack: bad arguments");
+    return guarded([&] {
+        *managed = tensorToDLPack(t, on_device != 0);
+        return ok();
+    });
+}
+
+int camel_tensor_from_dlpack(const DLManagedTensor *managed, uint64_t *handle) {
+    if (!handle) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_from_dlpack: bad arguments");
+    return guarded([&] {
+        *handle = toSlot(tensorFromDLPack(managed));
+        return ok();
+    });
+}
+
 int64_t camel_tensor_live_count(void) { return (int64_t)liveTensorCount(); }
 
 int64_t camel_tensor_release_all(void) { return (int64_t)releaseAll(); }

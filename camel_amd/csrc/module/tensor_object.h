@@ -17,6 +17,7 @@
 #pragma once
 
 #include "camel_core.h"
+#include "camel_dlpack.h"
 
 #include <cstddef>
 #include <iosfwd>
@@ -83,6 +84,8 @@ class TensorObject {
 
     bool hostValid() const;
     bool deviceValid() const;
+    // The payload block, shared with views and with DLPack exports.
+    const std::shared_ptr<Storage> &storage() const { return storage_; }
 
     // Element access with the reference's conversions (runtime.cpp:298-389).
     // A device-only tensor is not downloaded whole: one element is copied.
@@ -129,6 +132,11 @@ double scalarToDouble(TypeCode code, slot_t value);
 std::vector<int64_t> parseShapeArray(const ArrayObject *shapeArray, TypeCode shapeCode);
 ArrayObject *makeShapeArray(const TensorObject *tensor);
 TensorObject *tensorFromArray(slot_t slot, TypeCode valueCode);
+
+// DLPack exchange (runtime.cpp:1079-1124): host copy or zero-copy device
+// export, and a copying import from host or device memory.
+DLManagedTensor *tensorToDLPack(const TensorObject *tensor, bool onDevice);
+TensorObject *tensorFromDLPack(const DLManagedTensor *managed);
 
 // Tensor-lifetime bookkeeping: every TensorObject / ArrayObject made by this
 // layer is registered so a host program (or a graph's end) can release it.

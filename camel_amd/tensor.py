@@ -45,6 +45,31 @@ class Value(C.Structure):
 
 
 _U64, _I64, _U32, _P = C.c_uint64, C.c_int64, C.c_uint32, C.c_void_p
+
+
+# DLPack v0.8 structs (include/camel_dlpack.h)
+class DLDevice(C.Structure):
+    _fields_ = [("device_type", C.c_int32), ("device_id", C.c_int32)]
+
+
+class DLDataType(C.Structure):
+    _fields_ = [("code", C.c_uint8), ("bits", C.c_uint8), ("lanes", C.c_uint16)]
+
+
+class DLTensor(C.Structure):
+    _fields_ = [("data", _P), ("device", DLDevice), ("ndim", C.c_int32), ("dtype", DLDataType),
+                ("shape", C.POINTER(_I64)), ("strides", C.POINTER(_I64)),
+                ("byte_offset", C.c_uint64)]
+
+
+class DLManagedTensor(C.Structure):
+    pass
+
+
+_DELETER = C.CFUNCTYPE(None, C.POINTER(DLManagedTensor))
+DLManagedTensor._fields_ = [("dl_tensor", DLTensor), ("manager_ctx", _P), ("deleter", _DELETER)]
+KDL_CPU, KDL_ROCM = 1, 10
+
 _SIG = {
     "camel_tensor_last_error": ([], C.c_char_p),
     "camel_tensor_abi_version": ([], C.c_int),
@@ -69,7 +94,28 @@ _SIG = {
     "camel_tensor_op_name": ([_I64], C.c_char_p),
     "camel_tensor_group_count": ([], _I64),
     "camel_tensor_group_name": ([_I64], C.c_char_p),
+    "camel_tensor_to_dlpack": ([_U64, C.c_int, C.POINTER(C.POINTER(DLManagedTensor))], C.c_int),
+    "camel_tensor_from_dlpack": ([C.POINTER(DLManagedTensor), C.POINTER(_U64)], C.c_int),
 }
+
+# PyCapsule plumbing of the DLPack Python protocol: a capsule named
+# "dltensor" owns its managed tensor until a consumer renames it
+# "used_dltensor" (and then calls the deleter itself).
+_capsule_new = C.PYFUNCTYPE(C.py_object, _P, C.c_char_p, _P)(("PyCapsule_New", C.pythonapi))
+_capsule_get = C.PYFUNCTYPE(_P, C.py_object, C.c_char_p)(("PyCapsule_GetPointer", C.pythonapi))
+_capsule_set_name = C.PYFUNCTYPE(C.c_int, C.py_object, C.c_char_p)(("PyCapsule_SetName",
+                                                                     C.pythonapi))
+# Raw-pointer forms for the destructor, which receives the dying capsule.
+_capsule_valid_raw = C.PYFUNCTYPE(C.c_int, _P, C.c_char_p)(("PyCapsule_IsValid", C.pythonapi))
+_capsule_get_raw = C.PYFUNCTYPE(_P, _P, C.c_char_p)(("PyCapsule_GetPointer", C.pythonapi))
+
+
+@C.CFUNCTYPE(None, _P)
+def _capsule_destructor(capsule):
+    if _capsule_valid_raw(capsule, b"dltensor"):
+        managed = C.cast(_capsule_get_raw(capsule, b"dltensor"), C.POINTER(DLManagedTensor))
+        if managed and managed.contents.deleter:
+            managed.contents.deleter(managed)
 
 _lib = None
 
@@ -174,6 +220,39 @@ class Tensor:
         if self.handle:
             _check(load().camel_tensor_release(self.handle))
             self.handle = 0
+
+    # ---- DLPack -------------------------------------------------------------
+    def to_dlpack(self, on_device: bool = True):
+        """A "dltensor" capsule: the device payload itself (kDLROCM, no copy)
+        or a host copy (kDLCPU).  The payload is complete when this returns."""
+        m = C.POINTER(DLManagedTensor)()
+        _check(load().camel_tensor_to_dlpack(self.handle, 1 if on_device else 0, C.byref(m)))
+        return _capsule_new(C.cast(m, _P), b"dltensor", C.cast(_capsule_destructor, _P))
+
+    def __dlpack__(self, stream=None, max_version=None, dl_device=None, copy=None):
+        # Exports are synchronised with the library stream, so any consumer
+        # stream may read them.
+        return self.to_dlpack(on_device=True)
+
+    def __dlpack_device__(self):
+        dev = C.c_int()
+        from camel_amd import _hip
+        _hip.call("camel_hip_current_device", C.byref(dev))
+        return (KDL_ROCM, dev.value)
+
+    @staticmethod
+    def from_dlpack(obj) -> "Tensor":
+        """A copy of a DLPack tensor (an object with __dlpack__, or a
+        "dltensor" capsule), from host memory or from this device.  A device
+        producer must have finished writing it (synchronise its stream)."""
+        cap = obj.__dlpack__() if hasattr(obj, "__dlpack__") else obj
+        managed = C.cast(_capsule_get(cap, b"dltensor"), C.POINTER(DLManagedTensor))
+        h = _U64()
+        _check(load().camel_tensor_from_dlpack(managed, C.byref(h)))
+        _capsule_set_name(cap, b"used_dltensor")
+        if managed.contents.deleter:
+            managed.contents.deleter(managed)
+        return Tensor(h.value)
 
 
 class Array:

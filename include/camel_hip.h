@@ -61,6 +61,10 @@ enum camel_hip_epilogue { CAMEL_EPI_NONE = 0, CAMEL_EPI_BIAS = 1, CAMEL_EPI_RELU
  * No reference counterpart (the reference is CPU-only). */
 int camel_hip_init(int device);
 int camel_hip_device_count(int *count);
+/* The device the library runs on (initialising device 0 if nothing chose
+ * one), e.g. the device_id of an exported DLPack tensor.  No reference
+ * counterpart. */
+int camel_hip_current_device(int *device);
 /* Text of the last error on this thread ("" when none). */
 const char *camel_hip_last_error(void);
 /* Blocks until all enqueued work is done. */

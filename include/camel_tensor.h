@@ -27,6 +27,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "camel_dlpack.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -81,6 +83,28 @@ int64_t camel_tensor_live_count(void);
 int camel_tensor_format(uint64_t handle, char *buf, size_t cap, size_t *needed);
 /* TensorObject::equals: same dtype, shape and bytes. */
 int camel_tensor_equals(uint64_t a, uint64_t b, int *equal);
+
+/* ---- DLPack (tensorToDLPackCopy / tensorFromDLPackCopy, runtime.cpp:1079-1124) */
+/* Exports a tensor as a DLManagedTensor; the consumer calls its deleter.
+ * on_device = 0: a host copy (kDLCPU), as tensorToDLPackCopy does
+ *   (runtime.cpp:1079-1105).
+ * on_device = 1: the device payload itself (kDLROCM, device_id = the
+ *   library's device), without a copy.  The managed tensor holds a reference
+ *   to the payload, so the handle may be released before the deleter runs.
+ *   The library stream is synchronised first, so the data is complete for a
+ *   consumer on any stream.  Tensors are immutable: the consumer must not
+ *   write through it.
+ * Float32, Int64 and Bool tensors only ("Unsupported dtype for DLPack
+ * export" otherwise, as the reference). */
+int camel_tensor_to_dlpack(uint64_t handle, int on_device, DLManagedTensor **managed);
+/* Imports a copy of a DLPack tensor (tensorFromDLPackCopy,
+ * runtime.cpp:1107-1124), from kDLCPU or from kDLROCM memory of the
+ * library's device.  Float32 / Int64 / Bool with lanes 1; row-major with
+ * strides NULL or equal to the compact strides (what PyTorch exports),
+ * byte_offset 0; the reference's error texts otherwise.  A device source
+ * must be complete (its producer synchronised); the copy is finished when
+ * this returns.  The caller keeps `managed` (its deleter is not called). */
+int camel_tensor_from_dlpack(const DLManagedTensor *managed, uint64_t *handle);
 
 /* ---- arrays (shape arguments, array operands, shape() results) ----------- */
 int camel_array_create(uint32_t elem_code, int64_t count, const uint64_t *slots, uint64_t *handle);
