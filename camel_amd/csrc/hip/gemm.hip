@@ -844,41 +844,83 @@ __global__ void matmul_generic_kernel(int adt, const void *A, int bdt, const voi
 
 // ---- conv helpers ----------------------------------------------------------------
 
-// x [N][C][HW] -> xt [N][HW][C]: 32x32 tiles through LDS, one image per z.
-// The extra z slice (z == N) reorders the weights w [Co][C][KHW] ->
-// wt [Co][KHW][C] (K ordered (kh, kw, c)) in the same launch.
+// x [N][C][HW] -> xt [N][HW][C] through LDS, one image per grid z; the
+// extra z slice (z == N) reorders the weights w [Co][C][KHW] -> wt [Co][KHW][C]
+// (K ordered (kh, kw, c)) in the same launch.
+//   VEC (HW % 4 == 0, C % 4 == 0, 16-byte aligned): tiles of 32 channels x
+//   TP_VEC pixels, 16-byte global loads along pixels and 16-byte stores along
+//   channels, 4 of each per thread;
+//   otherwise 32 x 32 tiles of 4-byte accesses.
+constexpr int TP_VEC = 128;
+
+__device__ __forceinline__ void reorder_weights(const float *__restrict__ w, float *__restrict__ wt,
+                                                int Co, int C, int KHW) {
+    const int total = Co * C * KHW;
+    const int nthreads = gridDim.x * gridDim.y * blockDim.x;
+    for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += nthreads) {
+        const int co = i / (C * KHW), r = i - co * C * KHW;
+        const int c = r / KHW, khw = r - c * KHW;
+        wt[(size_t)co * C * KHW + (size_t)khw * C + c] = w[i];
+    }
+}
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const float *__restrict__ x,
                                                            float *__restrict__ xt, int C, int HW,
                                                            const float *__restrict__ w,
                                                            float *__restrict__ wt, int Co,
                                                            int KHW) {
-    __shared__ float tile[32][33];
+    constexpr int TP = VEC ? TP_VEC : 32, LD = TP + 1;
+    __shared__ float tile[32 * LD];
     if (blockIdx.z == gridDim.z - 1) {
-        const int total = Co * C * KHW;
-        const int nthreads = gridDim.x * gridDim.y * blockDim.x;
-        for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-             i += nthreads) {
-            const int co = i / (C * KHW), r = i - co * C * KHW;
-            const int c = r / KHW, khw = r - c * KHW;
-            wt[(size_t)co * C * KHW + (size_t)khw * C + c] = w[i];
-        }
+        reorder_weights(w, wt, Co, C, KHW);
         return;
     }
     const size_t img = blockIdx.z;
     const float *src = x + img * (size_t)C * HW;
     float *dst = xt + img * (size_t)C * HW;
-    const int p0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    const int p0 = blockIdx.x * TP, c0 = blockIdx.y * 32;
+    if constexpr (VEC) {
+        // load: item i -> channel c0 + i / (TP/4), pixels p0 + 4 (i % (TP/4)) .. +3
 #pragma unroll
-    for (int k = ty; k < 32; k += 8) {
-        const int c = c0 + k, p = p0 + tx;
-        if (c < C && p < HW) tile[k][tx] = src[(size_t)c * HW + p];
-    }
-    __syncthreads();
+        for (int u = 0; u < 32 * TP / 4 / 256; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            const int c = i / (TP / 4), p = 4 * (i % (TP / 4));
+            if (c0 + c < C && p0 + p < HW) {
+                const float4 v =
+                    *reinterpret_cast<const float4 *>(src + (size_t)(c0 + c) * HW + p0 + p);
+                tile[c * LD + p] = v.x;
+                tile[c * LD + p + 1] = v.y;
+                tile[c * LD + p + 2] = v.z;
+                tile[c * LD + p + 3] = v.w;
+            }
+        }
+        __syncthreads();
+        // store: item i -> pixel p0 + i / 8, channels c0 + 4 (i % 8) .. +3
 #pragma unroll
-    for (int k = ty; k < 32; k += 8) {
-        const int p = p0 + k, c = c0 + tx;
-        if (c < C && p < HW) dst[(size_t)p * C + c] = tile[tx][k];
+        for (int u = 0; u < 32 * TP / 4 / 256; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            const int p = i / 8, c = 4 * (i % 8);
+            if (p0 + p < HW && c0 + c < C) {
+                const float4 v = make_float4(tile[c * LD + p], tile[(c + 1) * LD + p],
+                                             tile[(c + 2) * LD + p], tile[(c + 3) * LD + p]);
+                *reinterpret_cast<float4 *>(dst + (size_t)(p0 + p) * C + c0 + c) = v;
+            }
+        }
+    } else {
+        const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+        for (int k = ty; k < 32; k += 8) {
+            const int c = c0 + k, p = p0 + tx;
+            if (c < C && p < HW) tile[k * LD + tx] = src[(size_t)c * HW + p];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = ty; k < 32; k += 8) {
+            const int p = p0 + k, c = c0 + tx;
+            if (c < C && p < HW) dst[(size_t)p * C + c] = tile[tx * LD + k];
+        }
     }
 }
 
@@ -1182,10 +1224,18 @@ int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int
     CAMEL_RETURN_IF(camel_hip_malloc(&xt, (size_t)(N * C * HW) * sizeof(float)));
     int rc = camel_hip_malloc(&wt, (size_t)(Co * K) * sizeof(float));
     if (rc == CAMEL_HIP_OK) {
-        dim3 tgrid((unsigned)((HW + 31) / 32), (unsigned)((C + 31) / 32), (unsigned)(N + 1));
-        hipLaunchKernelGGL(nchw_to_nhwc_kernel, tgrid, dim3(256), 0, stream(), x,
-                           static_cast<float *>(xt), (int)C, (int)HW, w, static_cast<float *>(wt),
-                           (int)Co, (int)(KH * KW));
+        // xt comes from the pool (256-byte aligned); x is 16-byte aligned here.
+        const bool vec = HW % 4 == 0 && C % 4 == 0;
+        const int tp = vec ? TP_VEC : 32;
+        dim3 tgrid((unsigned)((HW + tp - 1) / tp), (unsigned)((C + 31) / 32), (unsigned)(N + 1));
+        if (vec)
+            hipLaunchKernelGGL(nchw_to_nhwc_kernel<true>, tgrid, dim3(256), 0, stream(), x,
+                               static_cast<float *>(xt), (int)C, (int)HW, w,
+                               static_cast<float *>(wt), (int)Co, (int)(KH * KW));
+        else
+            hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, tgrid, dim3(256), 0, stream(), x,
+                               static_cast<float *>(xt), (int)C, (int)HW, w,
+                               static_cast<float *>(wt), (int)Co, (int)(KH * KW));
         rc = check_launch("nchw_to_nhwc_kernel");
     }
     if (rc == CAMEL_HIP_OK) {
