@@ -938,36 +938,42 @@ constexpr int DIRECT_MAX_K = 32;
 // registers.  EXACT (KMAX == C*KH*KW): no per-k guard, so the weight loads of
 // a channel batch into a few scalar loads (a guarded one becomes a branch
 // around a lone scalar load and its full latency).
-template <int KMAX, bool EXACT>
+// PIX consecutive output pixels per thread (P % PIX == 0, so they share an
+// image): the channel loop then stores PIX-wide vectors.
+template <int KMAX, bool EXACT, int PIX>
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(
     const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
     int stride, int pad, int flags) {
+    typedef float vecp __attribute__((ext_vector_type(PIX)));
     const int K = C * KH * KW;
-    const int pg = blockIdx.x * blockDim.x + threadIdx.x;
+    const int pg = (blockIdx.x * blockDim.x + threadIdx.x) * PIX;
     if (pg >= NP) return;
     const int img = pg / P, p = pg - img * P;
-    const int oh = p / OW, ow = p - oh * OW;
-    const int ih0 = oh * stride - pad, iw0 = ow * stride - pad;
     const float *xi = x + (size_t)img * C * H * W;
-    float xv[KMAX];
-    int c = 0, kh = 0, kw = 0;
+    float xv[PIX][KMAX];
 #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-        float v = 0.f;
-        if (EXACT || k < K) {
-            const int ih = ih0 + kh, iw = iw0 + kw;
-            if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
-                v = xi[(size_t)c * H * W + (size_t)ih * W + iw];
-            if (++kw == KW) {
-                kw = 0;
-                if (++kh == KH) {
-                    kh = 0;
-                    ++c;
+    for (int j = 0; j < PIX; ++j) {
+        const int oh = (p + j) / OW, ow = (p + j) - oh * OW;
+        const int ih0 = oh * stride - pad, iw0 = ow * stride - pad;
+        int c = 0, kh = 0, kw = 0;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+            float v = 0.f;
+            if (EXACT || k < K) {
+                const int ih = ih0 + kh, iw = iw0 + kw;
+                if ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                    v = xi[(size_t)c * H * W + (size_t)ih * W + iw];
+                if (++kw == KW) {
+                    kw = 0;
+                    if (++kh == KH) {
+                        kh = 0;
+                        ++c;
+                    }
                 }
             }
+            xv[j][k] = v;
         }
-        xv[k] = v;
     }
     float *yo = y + (size_t)img * Co * P + p;
     // Epilogue flags are fixed per variant so the channel loop has no
@@ -976,13 +982,18 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
 #pragma unroll 4
         for (int co = 0; co < Co; ++co) {
             const float *wr = w + (size_t)co * K;
-            float acc = 0.f;
+            vecp out;
 #pragma unroll
-            for (int k = 0; k < KMAX; ++k)
-                if (EXACT || k < K) acc = __builtin_fmaf(wr[k], xv[k], acc);
-            if constexpr (decltype(has_bias)::value) acc = acc + bias[co];
-            if constexpr (decltype(has_relu)::value) acc = relu_idiom(acc);
-            yo[(size_t)co * P] = acc;
+            for (int j = 0; j < PIX; ++j) {
+                float acc = 0.f;
+#pragma unroll
+                for (int k = 0; k < KMAX; ++k)
+                    if (EXACT || k < K) acc = __builtin_fmaf(wr[k], xv[j][k], acc);
+                if constexpr (decltype(has_bias)::value) acc = acc + bias[co];
+                if constexpr (decltype(has_relu)::value) acc = relu_idiom(acc);
+                out[j] = acc;
+            }
+            *reinterpret_cast<vecp *>(yo + (size_t)co * P) = out;
         }
     };
     using T_ = std::true_type;
@@ -1166,25 +1177,32 @@ int conv2d_direct(const float *x, const float *w, const float *bias, float *y, i
                   int64_t pad, int64_t OH, int64_t OW, int flags) {
     const int64_t P = OH * OW, NP = N * P;
     const int64_t K = C * KH * KW;
-    dim3 grid((unsigned)((NP + 255) / 256));
-    auto go = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream(), x, w, bias, y, (int)NP, (int)P,
-                           (int)OW, (int)C, (int)H, (int)W, (int)Co, (int)KH, (int)KW, (int)stride,
-                           (int)pad, flags);
+    // 2 pixels per thread (8-byte stores) when every channel plane of y
+    // stays 8-byte aligned (measured 2-4% faster than 1 or 4 at the CNN's
+    // first layer); 1 otherwise.
+    const bool pair = P % 2 == 0 && ((uintptr_t)y & 7) == 0;
+    auto go = [&](auto kernel, int pix) {
+        const int64_t threads = (NP + pix - 1) / pix;
+        hipLaunchKernelGGL(kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream(), x,
+                           w, bias, y, (int)NP, (int)P, (int)OW, (int)C, (int)H, (int)W, (int)Co,
+                           (int)KH, (int)KW, (int)stride, (int)pad, flags);
         return check_launch("conv2d_direct_kernel");
     };
     // Exact kernels for the usual first layers: 3x3 and 5x5 over 1 or 3
     // channels.
     if (K == 9)
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<9, true>));
+        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<9, true, 2>, 2)
+                             : go(conv2d_direct_kernel<9, true, 1>, 1));
     else if (K == 25)
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<25, true>));
+        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<25, true, 2>, 2)
+                             : go(conv2d_direct_kernel<25, true, 1>, 1));
     else if (K == 27)
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<27, true>));
+        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<27, true, 2>, 2)
+                             : go(conv2d_direct_kernel<27, true, 1>, 1));
     else if (K <= 16)
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<16, false>));
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<16, false, 1>, 1));
     else
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<DIRECT_MAX_K, false>));
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<DIRECT_MAX_K, false, 1>, 1));
     return ok();
 }
 

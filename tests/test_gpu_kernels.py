@@ -301,6 +301,10 @@ def test_conv2d_matches_oracle(N, Cin, H_, W_, Co, k, stride, pad):
     (2, 48, 7, 7, 150, 3, 3, 1, 1),     # NHWC path with C = 48 (3 stages per (kh, kw))
     (2, 12, 8, 8, 24, 3, 3, 1, 1),      # gather path: C % 16 != 0, K = 108
     (4, 2, 10, 10, 33, 4, 4, 2, 1),     # direct path, K = 32, Co not a multiple of 8
+    (2, 3, 16, 16, 16, 3, 3, 1, 1),     # direct, K = 27, 2 pixels per thread
+    (2, 3, 32, 32, 16, 3, 3, 2, 1),     # direct, K = 27, stride 2, 2 pixels per thread
+    (3, 1, 12, 12, 8, 5, 5, 1, 2),      # direct, K = 25, 2 pixels per thread
+    (2, 1, 13, 13, 7, 5, 5, 2, 0),      # direct, K = 25, P = 25: one pixel per thread
 ])
 def test_conv2d_paths_rect_kernels(N, Cin, H_, W_, Co, kh, kw, stride, pad):
     x = D.normal(910 + Cin, (N, Cin, H_, W_))
