@@ -84,6 +84,7 @@ struct GemmArgs {
     int lda, ldb, ldc;
     int k_per_split;  // multiple of BK
     int tile_begin;   // first logical tile of the launch
+    int n_begin;      // first column of the launch's tile grid (a column band)
     int flags;
     // conv geometry (N = batch * P columns); Cin, KW only for LOAD_NHWC
     int P, OW, H, W, CHW, stride, pad;
@@ -126,10 +127,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 
     const int tid = threadIdx.x;
     const int tiles_m = (g.M + T::BM - 1) / T::BM;
-    const int tiles_n = (g.N + T::BN - 1) / T::BN;
+    const int tiles_n = (g.N - g.n_begin + T::BN - 1) / T::BN;
     int tm, tn;
     tile_of(block_tile_id(g.tile_begin), tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * T::BM, n0 = tn * T::BN;
+    const int m0 = tm * T::BM, n0 = g.n_begin + tn * T::BN;
     const int kbeg = blockIdx.y * g.k_per_split;
     const int kend = min(g.K, kbeg + g.k_per_split);
     const int nk = kend > kbeg ? (kend - kbeg + T::BK - 1) / T::BK : 0;
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 // stores with the GEMM (row-major) or conv (NCHW) output mapping.
 template <int BM, int BN, bool CONV>
 __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles, int splits) {
-    const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + BN - 1) / BN;
+    const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N - g.n_begin + BN - 1) / BN;
     const size_t per_tile = (size_t)BM * BN, total = (size_t)ntiles * per_tile;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
@@ -533,7 +534,7 @@ __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles
         const int w = (int)(idx - (size_t)local * per_tile);
         int tm, tn;
         tile_of(g.tile_begin + local, tiles_m, tiles_n, tm, tn);
-        const int row = tm * BM + w / BN, col = tn * BN + w % BN;
+        const int row = tm * BM + w / BN, col = g.n_begin + tn * BN + w % BN;
         if (row >= g.M || col >= g.N) continue;
         float s = g.partial[idx];
         for (int z = 1; z < splits; ++z) s = s + g.partial[(size_t)z * total + idx];
@@ -1115,20 +1116,44 @@ int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char 
     return CAMEL_HIP_OK;
 }
 
+// Small tile for the column band left after the whole rounds (see run_gemm):
+// 64 x 32 with 4 waves (2 x 1 spatial x 2 k-groups, so all 4 SIMDs of a CU
+// work on it); 64 x 64 with 2 x 2 waves when BK = 16, which two k-groups
+// would not split into whole 8-k groups per register buffer.
+template <class T>
+using BandTile = Tile<64, (T::BK >= 32 ? 32 : 64), T::BK, 2, (T::BK >= 32 ? 1 : 2),
+                      (T::BK >= 32 ? 2 : 1)>;
+
 // Schedules all tiles.  `splits` > 1 splits every tile (small problems).
 // Otherwise whole rounds of resident work-groups run as whole tiles, and the
-// tiles of a last, partial round are split along K across the chip instead
-// of leaving most CUs idle for a whole tile time.
+// tiles of a last, partial round (when it is at most a quarter full) run so
+// that the whole chip shares them instead of leaving most CUs idle for a
+// whole tile time:
+//   * when every tile row sits in one tile-row group (tile id = tn * tiles_m
+//     + tm) the leftover tiles are whole tile columns, i.e. a column band,
+//     and that band runs as one launch of small tiles over all of K (no
+//     partials; measured faster than the split below at BASELINE config 4,
+//     whose 1568 tiles leave 32 after 3 rounds);
+//   * otherwise the leftover tiles are split along K and reduced in order.
 template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, const char *name) {
-    const int tiles = (int)(((int64_t)(g.M + T::BM - 1) / T::BM) * ((g.N + T::BN - 1) / T::BN));
+    const int tiles_m = (g.M + T::BM - 1) / T::BM;
+    const int tiles = (int)((int64_t)tiles_m * ((g.N + T::BN - 1) / T::BN));
     if (splits > 1) return launch_range<T, AMODE, BMODE>(g, 0, tiles, splits, name);
     const int slots = resident_slots<T, AMODE, BMODE>();
     const int stages = (g.K + T::BK - 1) / T::BK;
     const int full = tiles / slots, rem = tiles % slots;
-    if (full == 0 || rem == 0 || stages < 4)
+    if (full == 0 || rem == 0 || stages < 4 || rem * 4 > slots)
         return launch_range<T, AMODE, BMODE>(g, 0, tiles, 1, name);
     const int dp = full * slots;
     CAMEL_RETURN_IF((launch_range<T, AMODE, BMODE>(g, 0, dp, 1, name)));
+    if (tiles_m <= GROUP_M && rem % tiles_m == 0) {
+        using TB = BandTile<T>;
+        GemmArgs band = g;
+        band.n_begin = dp / tiles_m * T::BN;
+        const int band_tiles =
+            (int)((int64_t)((g.M + TB::BM - 1) / TB::BM) * ((g.N - band.n_begin + TB::BN - 1) / TB::BN));
+        return launch_range<TB, AMODE, BMODE>(band, 0, band_tiles, 1, name);
+    }
     const int tail_splits = std::max(1, std::min(slots / rem, stages / 2));
     return launch_range<T, AMODE, BMODE>(g, dp, rem, tail_splits, name);
 }

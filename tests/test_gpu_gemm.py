@@ -106,6 +106,20 @@ def test_partial_round_is_split_along_k():
         assert ok, f"rows {r0}-{r1}: worst error / bound = {worst}"
 
 
+def test_partial_round_column_band():
+    # M = 512 in 256x256 tiles: 2 tile rows in one group, so the 2 tiles left
+    # after a whole round (N = 33024 -> 129 tile columns) are the last tile
+    # column, run as a band of 64x32 tiles over all of K.
+    m, n, k = 512, 33024, 256
+    a, b = _ab(m, n, k, D.SEED_GEMM + 9)
+    bias = D.uniform(D.SEED_GEMM + 10, (n,), -1.0, 1.0)
+    got = K.sgemm(a, b, bias, H.EPI_BIAS | H.EPI_RELU)
+    for r0, r1 in ((0, 6), (250, 262), (m - 6, m)):
+        ref = O.dense(a[r0:r1], b, bias, True)
+        ok, worst = K.gemm_tol_ok(got[r0:r1], ref, a[r0:r1], b)
+        assert ok, f"rows {r0}-{r1}: worst error / bound = {worst}"
+
+
 def test_skinny_gemm_matches_oracle():
     a, b = _ab(16, 4096, 4096, D.SEED_GEMM + 16)
     got = K.sgemm(a, b)
