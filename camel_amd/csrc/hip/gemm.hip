@@ -1,27 +1,34 @@
-// fp32 GEMM and implicit-GEMM conv2d on gfx950 MFMA (v_mfma_f32_32x32x2_f32).
+// fp32 GEMM and implicit-GEMM conv2d on gfx950 MFMA.
 //
 // Replaces the ijk double loop of __tensor_matmul__
 // (modules/tensor/operators.cpp:757-766) and defines conv2d / dense on the
 // same core.
 //
-// Kernel structure (one template, three operand loaders):
-//   * workgroup tile BM x BN, K consumed in stages of BK; 4 waves in a
-//     WM x WN grid, each wave owns (BM/WM) x (BN/WN) = FM x FN blocks of 32x32;
+// Main kernel (sgemm_kernel: one template, four operand loaders,
+// v_mfma_f32_32x32x2_f32):
+//   * work-group tile BM x BN, K consumed in stages of BK; WM x WN waves, each
+//     owning (BM/WM) x (BN/WN) = FM x FN blocks of 32x32, optionally times WK
+//     k-groups that split each stage's K and meet in LDS at the end;
 //   * LDS holds both operands "k-quad major": plane q holds, for every row of
 //     the tile, the 4 consecutive k values 4q..4q+3 as one 16-byte chunk, so a
 //     lane fetches its 4 k values of a 32x32 block with one ds_read_b128;
-//     planes are padded by 16 bytes to spread the stores over the banks;
+//     planes are padded by 16 bytes, and B columns are XOR-swizzled (b_slot),
+//     so that the stores and the operand reads are free of bank conflicts;
 //   * a 32x32x2 MFMA takes, per lane l, k = 8s + 4*(l/32) + t (t = 0..3) from
 //     that chunk: the lower half-wave covers k 0..3 of an 8-group, the upper
 //     half k 4..7, and A and B use the same mapping, so every k is summed once;
 //   * stages are double-buffered in LDS with the next stage held in registers
-//     while the current one is multiplied (one barrier per stage);
+//     while the current one is multiplied, one barrier per stage;
 //   * blockIdx is remapped so each of the 8 XCDs (own L2) works on a compact
 //     group of tiles, grouped GROUP_M tile-rows deep;
-//   * split-K (blockIdx.y) writes fp32 partials that a second kernel sums in
+//   * split-K (blockIdx.y) writes fp32 partials that tile_reduce_kernel sums in
 //     split order and passes through the epilogue;
 //   * epilogue: bias (per column for dense, per row = output channel for
 //     conv) then relu as x * (x > 0), stored straight from the accumulators.
+// Shapes the main kernel serves badly have their own kernels: N <= 32
+// (sgemm_thin_kernel, fp32 FMA) and M <= 32 (sgemm_skinny_kernel, a
+// streaming pass over B on v_mfma_f32_16x16x4_f32); conv2d with
+// C*KH*KW <= 32 runs conv2d_direct_kernel.
 #include "common.h"
 
 #include <algorithm>
@@ -1019,7 +1026,7 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
 using TileBig = Tile<256, 256, 32, 2, 4, 1, false>; // wave 128x64, 8 waves
 using TileMid = Tile<128, 128, 32, 2, 2>;           // wave 64x64
 using TileSmall = Tile<64, 64, 64, 2, 2, 2>;        // wave 32x32, two k-groups (8 waves)
-using TileSkinny = Tile<32, 128, 64, 1, 4>;  // wave 32x32, M <= 32
+using TileSkinny = Tile<32, 128, 64, 1, 4>;  // M <= 32 when the streaming kernel cannot run
 using TileConv = Tile<128, 128, 32, 2, 2>;   // NHWC conv, Co > 64, C % 32 == 0
 using TileConv16 = Tile<128, 128, 16, 2, 2>; // NHWC conv, Co > 64, C % 16 == 0
 using TileConv64 = Tile<64, 128, 32, 2, 2>;  // NHWC conv, Co <= 64, C % 32 == 0
