@@ -675,98 +675,121 @@ int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, c
 
 // Skinny GEMM (M <= 32, e.g. M = 16, N = K = 4096): B is read once from HBM
 // and dominates the traffic, so the kernel is a streaming pass over B.
-//   * a work-group owns 64 columns x SK_KB k, its 8 waves SK_KB / 8 k each;
-//     per 4-k step lane l loads one 16-byte chunk of B row k0 + 4s + l/16,
-//     columns n0 + 4 (l % 16) .. +3, so 16 lanes cover 256 contiguous bytes
-//     of a row; the wave's B loads are all issued before A is staged;
+//   * a work-group owns 64 columns x SK_CHUNK * CH k; its 8 waves take
+//     interleaved chunks (wave w, chunk c: rows kb0 + (8 c + w) * 32 .. +31),
+//     so at any time the work-group reads one contiguous block of rows;
+//   * within a chunk lane l takes rows base + 8 (l / 16) + s (s = 0..7) and
+//     one 16-byte piece of each, columns n0 + 4 (l % 16) .. +3: one load
+//     instruction covers 4 rows x 256 contiguous bytes;
 //   * v_mfma_f32_16x16x4_f32 takes A[i][k] from lane i + 16 k and B[k][j]
-//     from lane j + 16 k; the 4 floats of a lane's chunk feed 4 MFMAs whose
+//     from lane j + 16 k; the 4 floats of a lane's piece feed 4 MFMAs whose
 //     column j stands for column n0 + 4 j + c (c = 0..3), so no shuffle is
 //     needed; the accumulator of MFMA c holds rows 4 (l / 16) + v at column
-//     n0 + 4 (l % 16) + c;
-//   * the work-group's A panel (rows x SK_KB) is staged in LDS with
-//     coalesced loads (per-lane A loads of 16 rows x 4 k cost more);
+//     n0 + 4 (l % 16) + c.  Lane l's 8 k of a chunk are contiguous, so its A
+//     values are two 16-byte loads (A is small and stays in L2);
+//   * chunk c + 1 is in flight while chunk c is multiplied (register double
+//     buffer; scheduling barriers keep the compiler from sinking the loads
+//     next to their use);
 //   * the 8 waves' sums meet in LDS in wave order; work-groups along K
 //     (blockIdx.y) write partials [ks][M][N] that skinny_reduce_kernel sums
 //     in ks order before the epilogue (letting the last work-group of a
-//     strip do it needs device-scope fences, and each one writes back and
-//     invalidates the XCD's L2: measured several times slower).
+//     strip do it needs device-scope release/acquire fences, and on this
+//     chip each one writes back or invalidates an XCD's whole L2: measured
+//     several times slower).
+// Work-groups whose rows, columns or k run past the operands take the same
+// loop with guarded scalar loads (a guarded load compiles to a branch, after
+// which the compiler waits for all loads at once, so full work-groups keep
+// the guard-free path).
 constexpr int SK_WAVES = 8;
 constexpr int SK_COLS = 64;
-constexpr int SK_STEPS = 8;                     // 4-k steps per wave
-constexpr int SK_KB = SK_WAVES * 4 * SK_STEPS;  // k per work-group
+constexpr int SK_STEPS = 8;                          // 4-row MFMA steps per chunk and wave
+constexpr int SK_CHUNK = SK_WAVES * 4 * SK_STEPS;    // k rows per chunk of the work-group
+constexpr int SK_MAX_KGROUPS = 65535;                // grid.y limit
 
-template <int MT>
+template <int MT, int CH>
 __global__ __launch_bounds__(SK_WAVES * 64) void sgemm_skinny_kernel(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N,
-    int K, const float *__restrict__ bias, int flags, float *__restrict__ partial) {
+    int K, const float *__restrict__ bias, int flags, float *__restrict__ partial, int a_vec) {
     typedef float floatx4 __attribute__((ext_vector_type(4)));
-    constexpr int STEPS = SK_STEPS, KW = 4 * STEPS, KB = SK_KB;
-    constexpr int AS = KB + 4; // LDS row stride of the A panel
-    __shared__ __attribute__((aligned(16))) float as[16 * MT * AS];
+    constexpr int S = SK_STEPS, KR = SK_CHUNK * CH;
     __shared__ float4 red[SK_WAVES][MT * 4][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, q = lane >> 4;
     const int strip = blockIdx.x, ks = blockIdx.y, nks = gridDim.y;
     const int n0 = strip * SK_COLS;
-    const int kb0 = ks * KB;
-    const int k0 = kb0 + wave * KW + q;
+    const int kb0 = ks * KR;
+    const int krow0 = kb0 + wave * 4 * S + q * S; // lane's first k of chunk 0
     const int col = n0 + 4 * r16;
-    const bool col_ok = col < N; // N % 4 == 0: a chunk is all in or all out
 
-    // FULL (every row, column and k in range, the common case) has no
-    // guards: a guarded load compiles to a branch, after which the compiler
-    // waits for all loads at once instead of one by one.
-    float4 b[STEPS];
-    auto load_b = [&](auto full_tag) {
-        constexpr bool FULL = decltype(full_tag)::value;
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) {
-            const int k = k0 + 4 * s;
-            b[s] = (FULL || (col_ok && k < K))
-                       ? *reinterpret_cast<const float4 *>(B + (size_t)k * N + col)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    const bool full = n0 + SK_COLS <= N && kb0 + KB <= K;
-    if (full)
-        load_b(std::true_type{});
-    else
-        load_b(std::false_type{});
-    if (full && M >= 16 * MT && (K & 3) == 0 && ((uintptr_t)A & 15) == 0) {
-        // 16-byte chunks, no guards
-#pragma unroll
-        for (int i = threadIdx.x; i < 16 * MT * KB / 4; i += SK_WAVES * 64) {
-            const int m = i / (KB / 4), kk = 4 * (i - m * (KB / 4));
-            *reinterpret_cast<float4 *>(as + m * AS + kk) =
-                *reinterpret_cast<const float4 *>(A + (size_t)m * K + kb0 + kk);
-        }
-    } else {
-        for (int i = threadIdx.x; i < 16 * MT * KB; i += SK_WAVES * 64) {
-            const int m = i / KB, kk = i - m * KB, k = kb0 + kk;
-            as[m * AS + kk] = (m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
-        }
-    }
-    __syncthreads();
-    float a[MT][STEPS];
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) a[t][s] = as[(16 * t + r16) * AS + wave * KW + q + 4 * s];
     floatx4 acc[MT][4];
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[t][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto stream_k = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        float4 b[2][S];
+        float4 a[2][MT][S / 4];
+        auto load = [&](int buf, int c) {
+            const int kc = krow0 + c * SK_CHUNK;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s)
+            for (int t = 0; t < MT; ++t) {
+                const int row = 16 * t + r16;
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].x, acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].y, acc[t][1], 0, 0, 0);
-            acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].z, acc[t][2], 0, 0, 0);
-            acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s], b[s].w, acc[t][3], 0, 0, 0);
+                for (int j = 0; j < S / 4; ++j) {
+                    const int k = kc + 4 * j;
+                    if (FULL) {
+                        a[buf][t][j] = *reinterpret_cast<const float4 *>(A + (size_t)row * K + k);
+                    } else {
+                        float e[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            e[i] = (row < M && k + i < K) ? A[(size_t)row * K + k + i] : 0.f;
+                        a[buf][t][j] = make_float4(e[0], e[1], e[2], e[3]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int k = kc + s;
+                b[buf][s] = (FULL || (col < N && k < K))
+                                ? *reinterpret_cast<const float4 *>(B + (size_t)k * N + col)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        };
+        auto multiply = [&](int buf) {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const float4 a4 = a[buf][t][s / 4];
+                    const float av = (s % 4 == 0) ? a4.x : (s % 4 == 1) ? a4.y : (s % 4 == 2) ? a4.z : a4.w;
+                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].x, acc[t][0], 0, 0, 0);
+                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].y, acc[t][1], 0, 0, 0);
+                    acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].z, acc[t][2], 0, 0, 0);
+                    acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].w, acc[t][3], 0, 0, 0);
+                }
+        };
+        load(0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < CH; c += 2) {
+            if (c + 1 < CH) load(1, c + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 2 < CH) load(0, c + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 1 < CH) multiply(1);
+            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    if (a_vec && n0 + SK_COLS <= N && kb0 + KR <= K)
+        stream_k(std::true_type{});
+    else
+        stream_k(std::false_type{});
+
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -778,60 +801,71 @@ __global__ __launch_bounds__(SK_WAVES * 64) void sgemm_skinny_kernel(
     // Thread x < MT*4*64 owns accumulator slot (t, c) of lane x % 64: rows
     // 16 t + 4 (l / 16) + v, column n0 + 4 (l % 16) + c.
     const int x = threadIdx.x;
-    const bool owner = x < MT * 4 * 64;
+    if (x >= MT * 4 * 64) return;
     const int slot = x >> 6, sl = x & 63;
     const int t = slot >> 2, c = slot & 3;
     const int row0 = 16 * t + 4 * (sl >> 4), ocol = n0 + 4 * (sl & 15) + c;
+    if (ocol >= N) return;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (owner) {
 #pragma unroll
-        for (int w = 0; w < SK_WAVES; ++w) {
-            const float4 p = red[w][slot][sl];
-            v[0] += p.x;
-            v[1] += p.y;
-            v[2] += p.z;
-            v[3] += p.w;
-        }
+    for (int w = 0; w < SK_WAVES; ++w) {
+        const float4 p = red[w][slot][sl];
+        v[0] += p.x;
+        v[1] += p.y;
+        v[2] += p.z;
+        v[3] += p.w;
     }
-    auto finish = [&](const float *vals) {
-        if (!owner || ocol >= N) return;
+    if (nks == 1) {
         const float bcol = (flags & CAMEL_EPI_BIAS) ? bias[ocol] : 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = row0 + i;
             if (row >= M) continue;
-            float y = vals[i];
+            float y = v[i];
             if (flags & CAMEL_EPI_BIAS) y = y + bcol;
             if (flags & CAMEL_EPI_RELU) y = relu_idiom(y);
             C[(size_t)row * N + ocol] = y;
         }
-    };
-    if (nks == 1) {
-        finish(v);
         return;
     }
     // partial layout [ks][M][N]
-    if (owner && ocol < N) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = row0 + i;
-            if (row < M) partial[((size_t)ks * M + row) * N + ocol] = v[i];
-        }
+    for (int i = 0; i < 4; ++i) {
+        const int row = row0 + i;
+        if (row < M) partial[((size_t)ks * M + row) * N + ocol] = v[i];
     }
 }
 
-// Sums the skinny kernel's k partials in ks order, then bias and relu.
-__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float *__restrict__ partial,
-                                                            float *__restrict__ C, int M, int N,
+// Sums the skinny kernel's k partials in ks order, then bias and relu; one
+// thread per 4 consecutive outputs of a row (N % 4 == 0).
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float4 *__restrict__ partial,
+                                                            float4 *__restrict__ C, int M, int N,
                                                             int nks, const float *__restrict__ bias,
                                                             int flags) {
-    const size_t total = (size_t)M * N;
+    const size_t total4 = (size_t)M * N / 4;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= total) return;
-    float y = partial[idx];
-    for (int z = 1; z < nks; ++z) y = y + partial[(size_t)z * total + idx];
-    if (flags & CAMEL_EPI_BIAS) y = y + bias[idx % N];
-    if (flags & CAMEL_EPI_RELU) y = relu_idiom(y);
+    if (idx >= total4) return;
+    float4 y = partial[idx];
+    for (int z = 1; z < nks; ++z) {
+        const float4 p = partial[(size_t)z * total4 + idx];
+        y.x = y.x + p.x;
+        y.y = y.y + p.y;
+        y.z = y.z + p.z;
+        y.w = y.w + p.w;
+    }
+    if (flags & CAMEL_EPI_BIAS) {
+        const size_t col = (idx * 4) % (size_t)N;
+        y.x = y.x + bias[col];
+        y.y = y.y + bias[col + 1];
+        y.z = y.z + bias[col + 2];
+        y.w = y.w + bias[col + 3];
+    }
+    if (flags & CAMEL_EPI_RELU) {
+        y.x = relu_idiom(y.x);
+        y.y = relu_idiom(y.y);
+        y.z = relu_idiom(y.z);
+        y.w = relu_idiom(y.w);
+    }
     C[idx] = y;
 }
 
@@ -1058,26 +1092,47 @@ int ensure_partial(size_t bytes) {
 }
 
 // True when the streaming skinny kernel serves C[M, N] = A[M, K] B[K, N].
-bool skinny_eligible(int64_t M, int64_t N, int64_t K, const float *B) {
-    return M <= 32 && K > 0 && N % 4 == 0 && ((uintptr_t)B & 15) == 0;
+bool skinny_eligible(int64_t M, int64_t N, int64_t K, const float *B, const float *C) {
+    return M <= 32 && K > 0 && N % 4 == 0 && ((uintptr_t)B & 15) == 0 &&
+           ((uintptr_t)C & 15) == 0 && (K + SK_CHUNK - 1) / SK_CHUNK <= SK_MAX_KGROUPS;
 }
 
 int launch_skinny(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
                   int flags) {
     const int strips = (N + SK_COLS - 1) / SK_COLS;
-    auto go = [&](auto kernel) -> int {
-        const int nks = (K + SK_KB - 1) / SK_KB;
+    // Chunks per work-group: the most that still leaves one work-group per
+    // CU (fewer, longer streams measured faster than more, shorter ones).
+    const int cus = std::max(1, device_cu_count());
+    int ch = 1;
+    for (int c : {4, 2}) {
+        if ((int64_t)strips * ((K + SK_CHUNK * c - 1) / (SK_CHUNK * c)) >= cus) {
+            ch = c;
+            break;
+        }
+    }
+    const int mt = M <= 16 ? 1 : 2;
+    const int a_vec = M >= 16 * mt && K % 4 == 0 && ((uintptr_t)A & 15) == 0;
+    auto go = [&](auto kernel, int chunks) -> int {
+        const int nks = (K + SK_CHUNK * chunks - 1) / (SK_CHUNK * chunks);
         if (nks > 1) CAMEL_RETURN_IF(ensure_partial((size_t)nks * M * N * sizeof(float)));
         hipLaunchKernelGGL(kernel, dim3((unsigned)strips, (unsigned)nks), dim3(SK_WAVES * 64), 0,
-                           stream(), A, B, C, M, N, K, bias, flags, g_partial);
+                           stream(), A, B, C, M, N, K, bias, flags, g_partial, a_vec);
         CAMEL_RETURN_IF(check_launch("sgemm_skinny_kernel"));
         if (nks == 1) return CAMEL_HIP_OK;
-        const int64_t total = (int64_t)M * N;
-        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                           stream(), g_partial, C, M, N, nks, bias, flags);
+        const int64_t total4 = (int64_t)M * N / 4;
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((total4 + 255) / 256)), dim3(256),
+                           0, stream(), reinterpret_cast<const float4 *>(g_partial),
+                           reinterpret_cast<float4 *>(C), M, N, nks, bias, flags);
         return check_launch("skinny_reduce_kernel");
     };
-    return M <= 16 ? go(sgemm_skinny_kernel<1>) : go(sgemm_skinny_kernel<2>);
+    if (mt == 1) {
+        if (ch == 4) return go(sgemm_skinny_kernel<1, 4>, 4);
+        if (ch == 2) return go(sgemm_skinny_kernel<1, 2>, 2);
+        return go(sgemm_skinny_kernel<1, 1>, 1);
+    }
+    if (ch == 4) return go(sgemm_skinny_kernel<2, 4>, 4);
+    if (ch == 2) return go(sgemm_skinny_kernel<2, 2>, 2);
+    return go(sgemm_skinny_kernel<2, 1>, 1);
 }
 
 // Work-groups of one kernel that fit on the chip at once (occupancy x CUs).
@@ -1381,7 +1436,7 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
         CAMEL_RETURN_IF(launch_thin(A, B, C, (int)M, (int)N, (int)K, bias, flags));
         return ok();
     }
-    if (skinny_eligible(M, N, K, B)) {
+    if (skinny_eligible(M, N, K, B, C)) {
         CAMEL_RETURN_IF(launch_skinny(A, B, C, (int)M, (int)N, (int)K, bias, flags));
         return ok();
     }

@@ -134,6 +134,10 @@ def test_skinny_gemm_matches_oracle():
     (17, 64, 5000),     # one strip, many k work-groups
     (3, 8, 7),          # one work-group, no partials
     (16, 256, 65536),   # 64 k work-groups per strip
+    (16, 4096, 2048),   # two chunks per work-group, every work-group guard-free
+    (32, 4096, 4096),   # two 16-row groups, four chunks per work-group
+    (16, 1024, 4099),   # K % 4 != 0: every work-group takes the guarded loads
+    (8, 2048, 8192),    # M < 16: rows past M read as zero
 ])
 def test_skinny_streaming_kernel_matches_oracle(M, N, Kd):
     # M <= 32, N % 4 == 0: the streaming kernel (16x16x4 MFMA), k partials
