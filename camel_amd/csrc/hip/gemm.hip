@@ -30,6 +30,7 @@
 // streaming pass over B on v_mfma_f32_16x16x4_f32); conv2d with
 // C*KH*KW <= 32 runs conv2d_direct_kernel.
 #include "common.h"
+#include "row_softmax.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -45,9 +46,12 @@ constexpr int GROUP_M = 4;
 // Operand loader kinds.  LOAD_CONV gathers im2col columns from NCHW x one
 // float at a time; LOAD_NHWC reads x in NHWC with K ordered (kh, kw, c), so
 // each k-quad of a pixel is one 16-byte load (needs C % BK == 0).
-enum { LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3 };
+// LOAD_NHWC_POOL is LOAD_NHWC with the columns in pool-window order and a
+// 2x2 max-pool epilogue (the fused conv2d..maxpool2d).
+enum { LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3, LOAD_NHWC_POOL = 4 };
 
-template <int M> constexpr bool is_conv = (M == LOAD_CONV || M == LOAD_NHWC);
+template <int M> constexpr bool is_nhwc = (M == LOAD_NHWC || M == LOAD_NHWC_POOL);
+template <int M> constexpr bool is_conv = (M == LOAD_CONV || is_nhwc<M>);
 
 // WK > 1 splits each stage's K range over WK groups of WM x WN waves (more
 // waves per CU to hide latency when there are few tiles); the groups' sums
@@ -96,6 +100,10 @@ struct GemmArgs {
     // conv geometry (N = batch * P columns); Cin, KW only for LOAD_NHWC
     int P, OW, H, W, CHW, stride, pad;
     int Cin, KW;
+    // LOAD_NHWC_POOL: columns in pool order, 4 per window of a 2x2 stride-2
+    // max pool over a PH x PW grid (PP = PH * PW windows per image); C is the
+    // pooled output [batch][M][PP]
+    int PW, PP;
 };
 
 // LDS slot of B column n within a k-quad plane.  A 16-byte LDS access is
@@ -142,7 +150,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     const int kend = min(g.K, kbeg + g.k_per_split);
     const int nk = kend > kbeg ? (kend - kbeg + T::BK - 1) / T::BK : 0;
 
-    if constexpr (BMODE == LOAD_NHWC) {
+    if constexpr (is_nhwc<BMODE>) {
         static_assert((T::BN * T::KQ) % T::THREADS == 0, "B pixel rows must split evenly");
     } else {
         static_assert(T::THREADS % (T::BN / 4) == 0 || (T::BN / 4) % T::THREADS == 0,
@@ -155,25 +163,37 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     // One stage of operands in flight from global memory to LDS.
     struct StageRegs {
         float4 ra[T::A_ITEMS];
-        float4 rb[BMODE == LOAD_NHWC ? 1 : T::B_ITEMS][4];
-        float4 rbn[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
+        float4 rb[is_nhwc<BMODE> ? 1 : T::B_ITEMS][4];
+        float4 rbn[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
     };
     StageRegs R0;
 
     // ---- NHWC conv: each thread's B items are fixed (pixel, k-quad) pairs.
     // Pixel geometry is decoded once; the k-quad's (kh, kw, c) comes from the
     // stage start (uniform: one stage never crosses a (kh, kw) boundary).
-    int px_base[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
-    int px_ih[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
-    int px_iw[BMODE == LOAD_NHWC ? T::BN_ITEMS : 1];
-    if constexpr (BMODE == LOAD_NHWC) {
+    int px_base[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
+    int px_ih[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
+    int px_iw[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
+    if constexpr (is_nhwc<BMODE>) {
 #pragma unroll
         for (int i = 0; i < T::BN_ITEMS; ++i) {
             const int q = tid + i * T::THREADS;
             const int pg = n0 + q / T::KQ;
             if (pg < g.N) {
-                const int img = pg / g.P, p = pg - img * g.P;
-                const int oh = p / g.OW, ow = p - oh * g.OW;
+                int img, oh, ow;
+                if constexpr (BMODE == LOAD_NHWC_POOL) {
+                    // column = ((img * PP + window) * 4 + 2 dy + dx)
+                    img = pg / (4 * g.PP);
+                    const int r = pg - img * 4 * g.PP, win = r >> 2, d = r & 3;
+                    const int ph = win / g.PW;
+                    oh = 2 * ph + (d >> 1);
+                    ow = 2 * (win - ph * g.PW) + (d & 1);
+                } else {
+                    img = pg / g.P;
+                    const int p = pg - img * g.P;
+                    oh = p / g.OW;
+                    ow = p - oh * g.OW;
+                }
                 px_ih[i] = oh * g.stride - g.pad;
                 px_iw[i] = ow * g.stride - g.pad;
                 px_base[i] = ((img * g.H + px_ih[i]) * g.W + px_iw[i]) * g.Cin;
@@ -234,7 +254,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 ra[i].w = (rv && (FULL || gk + 3 < kend)) ? src[3] : 0.f;
             }
         }
-        if constexpr (BMODE == LOAD_NHWC) {
+        if constexpr (is_nhwc<BMODE>) {
             // k0 .. k0+BK-1 share (kh, kw): channels c0 .. c0+BK-1.
             const int khw = k0 / g.Cin, c0 = k0 - khw * g.Cin;
             const int kh = khw / g.KW, kw = khw - kh * g.KW;
@@ -251,7 +271,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < (BMODE == LOAD_NHWC ? 0 : T::B_ITEMS); ++i) {
+        for (int i = 0; i < (is_nhwc<BMODE> ? 0 : T::B_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             if (B_TAIL && q >= T::B_TOTAL) break;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
@@ -309,7 +329,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             const int kq = q % T::KQ, m = q / T::KQ;
             *reinterpret_cast<float4 *>(As + kq * T::A_PLANE + m * 4) = ra[i];
         }
-        if constexpr (BMODE == LOAD_NHWC) {
+        if constexpr (is_nhwc<BMODE>) {
 #pragma unroll
             for (int i = 0; i < T::BN_ITEMS; ++i) {
                 const int q = tid + i * T::THREADS;
@@ -318,7 +338,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < (BMODE == LOAD_NHWC ? 0 : T::B_ITEMS); ++i) {
+        for (int i = 0; i < (is_nhwc<BMODE> ? 0 : T::B_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             if (B_TAIL && q >= T::B_TOTAL) break;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
@@ -495,6 +515,41 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     // ---- epilogue ----
     const bool has_bias = (g.flags & CAMEL_EPI_BIAS) != 0 && g.partial == nullptr;
     const bool has_relu = (g.flags & CAMEL_EPI_RELU) != 0 && g.partial == nullptr;
+    if constexpr (BMODE == LOAD_NHWC_POOL) {
+        if (g.partial == nullptr) {
+            // A pool window is 4 consecutive columns, i.e. lanes r32 .. r32+3
+            // of one half-wave (window starts are multiples of 4).  Every lane
+            // takes part in the shuffles; the window's first lane stores the
+            // max in the order (0,0), (0,1), (1,0), (1,1) with a strict '>'
+            // (maxpool2x2_kernel's rule).  Rows and columns past the problem
+            // are uniform across a window.
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j) {
+                const int col = n0 + wn * T::WTN + j * 32 + r32;
+                const int img = col / (4 * g.PP), win = (col - img * 4 * g.PP) >> 2;
+                const bool store_col = col < g.N && (r32 & 3) == 0;
+#pragma unroll
+                for (int i = 0; i < T::FM; ++i) {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int row = m0 + wm * T::WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                        float x = acc[i][j][v];
+                        if (has_bias) x = x + (row < g.M ? g.bias[row] : 0.f);
+                        if (has_relu) x = relu_idiom(x);
+                        const float x1 = __shfl_down(x, 1), x2 = __shfl_down(x, 2),
+                                    x3 = __shfl_down(x, 3);
+                        float mx = x;
+                        if (x1 > mx) mx = x1;
+                        if (x2 > mx) mx = x2;
+                        if (x3 > mx) mx = x3;
+                        if (store_col && row < g.M)
+                            g.C[((size_t)img * g.M + row) * g.PP + win] = mx;
+                    }
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < T::FN; ++j) {
         const int col = n0 + wn * T::WTN + j * 32 + r32;
@@ -531,9 +586,36 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 // Sums the K splits of tiles [tile_begin, tile_begin + ntiles) in split
 // order (so results do not depend on scheduling), then bias and relu, and
 // stores with the GEMM (row-major) or conv (NCHW) output mapping.
-template <int BM, int BN, bool CONV>
+// POOL (pooled conv): one thread per pool window (4 consecutive columns of
+// a tile), max of the 4 finished values in window order.
+template <int BM, int BN, bool CONV, bool POOL = false>
 __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles, int splits) {
     const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N - g.n_begin + BN - 1) / BN;
+    if constexpr (POOL) {
+        const size_t per_tile = (size_t)BM * BN, total = (size_t)ntiles * per_tile;
+        const size_t stride = (size_t)gridDim.x * blockDim.x;
+        for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total / 4; q += stride) {
+            const size_t idx = 4 * q;
+            const int local = (int)(idx / per_tile);
+            const int w = (int)(idx - (size_t)local * per_tile);
+            int tm, tn;
+            tile_of(g.tile_begin + local, tiles_m, tiles_n, tm, tn);
+            const int row = tm * BM + w / BN, col = g.n_begin + tn * BN + w % BN;
+            if (row >= g.M || col >= g.N) continue;
+            float mx = 0.f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                float s = g.partial[idx + d];
+                for (int z = 1; z < splits; ++z) s = s + g.partial[(size_t)z * total + idx + d];
+                if (g.flags & CAMEL_EPI_BIAS) s = s + g.bias[row];
+                if (g.flags & CAMEL_EPI_RELU) s = relu_idiom(s);
+                if (d == 0 || s > mx) mx = s;
+            }
+            const int img = col / (4 * g.PP), win = (col - img * 4 * g.PP) >> 2;
+            g.C[((size_t)img * g.M + row) * g.PP + win] = mx;
+        }
+        return;
+    }
     const size_t per_tile = (size_t)BM * BN, total = (size_t)ntiles * per_tile;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
@@ -563,10 +645,12 @@ __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles
 // serves per cycle land on disjoint banks.  Each wave owns one row of A at a
 // time: lane l takes k = l + 64 i (coalesced loads, zero past K) and
 // accumulates all NT columns in fp32 FMA; a wave-shuffle tree sums the 64
-// partials; bias and relu as in the MFMA epilogue.
+// partials; bias and relu as in the MFMA epilogue.  SOFTMAX (the fused
+// dense..softmax of a classifier) then takes the row softmax across the
+// wave's lanes, lane c holding column c, before the store.
 constexpr int THIN_LDS_FLOATS = 20480; // 80 KiB of B per work-group
 
-template <int NT, int KV>
+template <int NT, int KV, bool SOFTMAX = false>
 __global__ __launch_bounds__(256) void sgemm_thin_kernel(const float *__restrict__ A,
                                                          const float *__restrict__ B,
                                                          float *__restrict__ C, int M, int N, int K,
@@ -635,8 +719,9 @@ __global__ __launch_bounds__(256) void sgemm_thin_kernel(const float *__restrict
         if (lane < N) {
             if (flags & CAMEL_EPI_BIAS) out = out + bias[lane];
             if (flags & CAMEL_EPI_RELU) out = relu_idiom(out);
-            C[(size_t)m * N + lane] = out;
         }
+        if constexpr (SOFTMAX) out = softmax_row_lanes(lane < N ? out : -INFINITY);
+        if (lane < N) C[(size_t)m * N + lane] = out;
     }
 }
 
@@ -647,6 +732,7 @@ bool thin_eligible(int64_t M, int64_t N, int64_t K) {
     return K <= (N <= 16 ? 1024 : 512);
 }
 
+template <bool SOFTMAX = false>
 int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
                 int flags) {
     // Enough waves to cover the rows once, at most one work-group per CU
@@ -660,17 +746,17 @@ int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, c
     };
     const int kv = std::max(1, (K + 255) / 256);
     if (N <= 8) {
-        if (kv <= 1) return go(sgemm_thin_kernel<8, 1>);
-        if (kv <= 2) return go(sgemm_thin_kernel<8, 2>);
-        return go(sgemm_thin_kernel<8, 4>);
+        if (kv <= 1) return go(sgemm_thin_kernel<8, 1, SOFTMAX>);
+        if (kv <= 2) return go(sgemm_thin_kernel<8, 2, SOFTMAX>);
+        return go(sgemm_thin_kernel<8, 4, SOFTMAX>);
     }
     if (N <= 16) {
-        if (kv <= 1) return go(sgemm_thin_kernel<16, 1>);
-        if (kv <= 2) return go(sgemm_thin_kernel<16, 2>);
-        return go(sgemm_thin_kernel<16, 4>);
+        if (kv <= 1) return go(sgemm_thin_kernel<16, 1, SOFTMAX>);
+        if (kv <= 2) return go(sgemm_thin_kernel<16, 2, SOFTMAX>);
+        return go(sgemm_thin_kernel<16, 4, SOFTMAX>);
     }
-    if (kv <= 1) return go(sgemm_thin_kernel<32, 1>);
-    return go(sgemm_thin_kernel<32, 2>);
+    if (kv <= 1) return go(sgemm_thin_kernel<32, 1, SOFTMAX>);
+    return go(sgemm_thin_kernel<32, 2, SOFTMAX>);
 }
 
 // Skinny GEMM (M <= 32, e.g. M = 16, N = K = 4096): B is read once from HBM
@@ -982,7 +1068,10 @@ constexpr int DIRECT_MAX_K = 32;
 // around a lone scalar load and its full latency).
 // PIX consecutive output pixels per thread (P % PIX == 0, so they share an
 // image): the channel loop then stores PIX-wide vectors.
-template <int KMAX, bool EXACT, int PIX>
+// YNHWC: y is [N][OH][OW][Co] (Co % 4 == 0, 16-byte aligned), for a consumer
+// that reads NHWC; channels go four at a time into one 16-byte store per
+// pixel, and every value is computed exactly as for the NCHW output.
+template <int KMAX, bool EXACT, int PIX, bool YNHWC = false>
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(
     const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
@@ -1021,6 +1110,30 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
     // Epilogue flags are fixed per variant so the channel loop has no
     // branches and its scalar loads batch across unrolled channels.
     auto channels = [&](auto has_bias, auto has_relu) {
+        if constexpr (YNHWC) {
+            float *yp = y + ((size_t)img * P + p) * Co;
+            for (int co = 0; co < Co; co += 4) {
+                float4 out[PIX];
+#pragma unroll
+                for (int c4 = 0; c4 < 4; ++c4) {
+                    const float *wr = w + (size_t)(co + c4) * K;
+#pragma unroll
+                    for (int j = 0; j < PIX; ++j) {
+                        float acc = 0.f;
+#pragma unroll
+                        for (int k = 0; k < KMAX; ++k)
+                            if (EXACT || k < K) acc = __builtin_fmaf(wr[k], xv[j][k], acc);
+                        if constexpr (decltype(has_bias)::value) acc = acc + bias[co + c4];
+                        if constexpr (decltype(has_relu)::value) acc = relu_idiom(acc);
+                        (c4 == 0 ? out[j].x : c4 == 1 ? out[j].y : c4 == 2 ? out[j].z : out[j].w) = acc;
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < PIX; ++j)
+                    *reinterpret_cast<float4 *>(yp + (size_t)j * Co + co) = out[j];
+            }
+            return;
+        }
 #pragma unroll 4
         for (int co = 0; co < Co; ++co) {
             const float *wr = w + (size_t)co * K;
@@ -1170,9 +1283,14 @@ int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char 
     CAMEL_RETURN_IF(check_launch(name));
     if (splits > 1) {
         const size_t total = (size_t)ntiles * T::BM * T::BN;
-        hipLaunchKernelGGL((tile_reduce_kernel<T::BM, T::BN, is_conv<BMODE>>),
-                           dim3(grid_for((int64_t)total, 256)), dim3(256), 0, stream(), g, ntiles,
-                           splits);
+        if (BMODE == LOAD_NHWC_POOL)
+            hipLaunchKernelGGL((tile_reduce_kernel<T::BM, T::BN, true, true>),
+                               dim3(grid_for((int64_t)total / 4, 256)), dim3(256), 0, stream(), g,
+                               ntiles, splits);
+        else
+            hipLaunchKernelGGL((tile_reduce_kernel<T::BM, T::BN, is_conv<BMODE>>),
+                               dim3(grid_for((int64_t)total, 256)), dim3(256), 0, stream(), g,
+                               ntiles, splits);
         CAMEL_RETURN_IF(check_launch("tile_reduce_kernel"));
     }
     return CAMEL_HIP_OK;
@@ -1261,13 +1379,14 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
 
 int conv2d_direct(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
                   int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
-                  int64_t pad, int64_t OH, int64_t OW, int flags) {
+                  int64_t pad, int64_t OH, int64_t OW, int flags, bool y_nhwc) {
     const int64_t P = OH * OW, NP = N * P;
     const int64_t K = C * KH * KW;
     // 2 pixels per thread (8-byte stores) when every channel plane of y
     // stays 8-byte aligned (measured 2-4% faster than 1 or 4 at the CNN's
-    // first layer); 1 otherwise.
-    const bool pair = P % 2 == 0 && ((uintptr_t)y & 7) == 0;
+    // first layer); 1 otherwise.  NHWC output (Co % 4 == 0, 16-byte aligned
+    // y) only needs the pixel pair inside one image.
+    const bool pair = P % 2 == 0 && (y_nhwc || ((uintptr_t)y & 7) == 0);
     auto go = [&](auto kernel, int pix) {
         const int64_t threads = (NP + pix - 1) / pix;
         hipLaunchKernelGGL(kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream(), x,
@@ -1275,23 +1394,53 @@ int conv2d_direct(const float *x, const float *w, const float *bias, float *y, i
                            (int)KH, (int)KW, (int)stride, (int)pad, flags);
         return check_launch("conv2d_direct_kernel");
     };
-    // Exact kernels for the usual first layers: 3x3 and 5x5 over 1 or 3
-    // channels.
-    if (K == 9)
-        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<9, true, 2>, 2)
-                             : go(conv2d_direct_kernel<9, true, 1>, 1));
-    else if (K == 25)
-        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<25, true, 2>, 2)
-                             : go(conv2d_direct_kernel<25, true, 1>, 1));
-    else if (K == 27)
-        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<27, true, 2>, 2)
-                             : go(conv2d_direct_kernel<27, true, 1>, 1));
-    else if (K <= 16)
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<16, false, 1>, 1));
-    else
-        CAMEL_RETURN_IF(go(conv2d_direct_kernel<DIRECT_MAX_K, false, 1>, 1));
+    auto pick = [&](auto ynhwc) -> int {
+        constexpr bool YN = decltype(ynhwc)::value;
+        // Exact kernels for the usual first layers: 3x3 and 5x5 over 1 or 3
+        // channels.
+        if (K == 9)
+            return pair ? go(conv2d_direct_kernel<9, true, 2, YN>, 2)
+                        : go(conv2d_direct_kernel<9, true, 1, YN>, 1);
+        if (K == 25)
+            return pair ? go(conv2d_direct_kernel<25, true, 2, YN>, 2)
+                        : go(conv2d_direct_kernel<25, true, 1, YN>, 1);
+        if (K == 27)
+            return pair ? go(conv2d_direct_kernel<27, true, 2, YN>, 2)
+                        : go(conv2d_direct_kernel<27, true, 1, YN>, 1);
+        if (K <= 16) return go(conv2d_direct_kernel<16, false, 1, YN>, 1);
+        return go(conv2d_direct_kernel<DIRECT_MAX_K, false, 1, YN>, 1);
+    };
+    CAMEL_RETURN_IF(y_nhwc ? pick(std::true_type{}) : pick(std::false_type{}));
     return ok();
 }
+
+// dst[n] = transpose of src[n] for n < N, each image an [A][B] matrix (NCHW
+// -> NHWC with A = channels, B = pixels; NHWC -> NCHW with A = pixels, B =
+// channels).  The transpose kernel's weight slice is given no weights.
+int transpose_images(const float *src, float *dst, int64_t N, int64_t A, int64_t B) {
+    if (N + 1 > 65535) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: batch too large for an NHWC layout");
+    const bool vec = A % 4 == 0 && B % 4 == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15) == 0;
+    const int tp = vec ? TP_VEC : 32;
+    dim3 grid((unsigned)((B + tp - 1) / tp), (unsigned)((A + 31) / 32), (unsigned)(N + 1));
+    if (vec)
+        hipLaunchKernelGGL(nchw_to_nhwc_kernel<true>, grid, dim3(256), 0, stream(), src, dst, (int)A,
+                           (int)B, nullptr, nullptr, 0, 1);
+    else
+        hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, grid, dim3(256), 0, stream(), src, dst,
+                           (int)A, (int)B, nullptr, nullptr, 0, 1);
+    return check_launch("nchw_to_nhwc_kernel");
+}
+
+// Pooled scratch owned for the duration of one entry point call (returned
+// to the stream-ordered pool on scope exit).
+struct Scratch {
+    void *p = nullptr;
+    ~Scratch() {
+        if (p) camel_hip_free(p);
+    }
+    int alloc(size_t bytes) { return camel_hip_malloc(&p, bytes); }
+    float *f() const { return static_cast<float *>(p); }
+};
 
 GemmArgs conv_args(const float *w, const float *x, const float *bias, float *y, int64_t N,
                    int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
@@ -1318,39 +1467,46 @@ GemmArgs conv_args(const float *w, const float *x, const float *bias, float *y, 
     return g;
 }
 
-// NHWC implicit GEMM: x is transposed to NHWC and w reordered to (kh, kw, c)
-// in pooled scratch (stream-ordered, returned to the pool after the launch).
+// NHWC implicit GEMM: x is transposed to NHWC (unless it already is) and w
+// reordered to (kh, kw, c) in pooled scratch (stream-ordered, returned to the
+// pool after the launch).  pool: y is the 2x2 stride-2 max pool of the
+// convolution, [N][Co][OH/2][OW/2], written from the GEMM epilogue.
 template <class T>
 int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
                 int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
-                int64_t pad, int64_t OH, int64_t OW, int flags) {
+                int64_t pad, int64_t OH, int64_t OW, int flags, bool x_nhwc, bool pool) {
     const int64_t HW = H * W, K = C * KH * KW;
-    void *xt = nullptr, *wt = nullptr;
-    CAMEL_RETURN_IF(camel_hip_malloc(&xt, (size_t)(N * C * HW) * sizeof(float)));
-    int rc = camel_hip_malloc(&wt, (size_t)(Co * K) * sizeof(float));
-    if (rc == CAMEL_HIP_OK) {
+    Scratch xt, wt;
+    CAMEL_RETURN_IF(wt.alloc((size_t)(Co * K) * sizeof(float)));
+    if (!x_nhwc) {
+        CAMEL_RETURN_IF(xt.alloc((size_t)(N * C * HW) * sizeof(float)));
         // xt comes from the pool (256-byte aligned); x is 16-byte aligned here.
         const bool vec = HW % 4 == 0 && C % 4 == 0;
         const int tp = vec ? TP_VEC : 32;
         dim3 tgrid((unsigned)((HW + tp - 1) / tp), (unsigned)((C + 31) / 32), (unsigned)(N + 1));
         if (vec)
-            hipLaunchKernelGGL(nchw_to_nhwc_kernel<true>, tgrid, dim3(256), 0, stream(), x,
-                               static_cast<float *>(xt), (int)C, (int)HW, w,
-                               static_cast<float *>(wt), (int)Co, (int)(KH * KW));
+            hipLaunchKernelGGL(nchw_to_nhwc_kernel<true>, tgrid, dim3(256), 0, stream(), x, xt.f(),
+                               (int)C, (int)HW, w, wt.f(), (int)Co, (int)(KH * KW));
         else
-            hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, tgrid, dim3(256), 0, stream(), x,
-                               static_cast<float *>(xt), (int)C, (int)HW, w,
-                               static_cast<float *>(wt), (int)Co, (int)(KH * KW));
-        rc = check_launch("nchw_to_nhwc_kernel");
+            hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, tgrid, dim3(256), 0, stream(), x, xt.f(),
+                               (int)C, (int)HW, w, wt.f(), (int)Co, (int)(KH * KW));
+    } else {
+        // weights only: a grid of one z slice is all weight slice
+        hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, dim3(grid_for(Co * K, 256), 1, 1), dim3(256),
+                           0, stream(), nullptr, nullptr, (int)C, (int)HW, w, wt.f(), (int)Co,
+                           (int)(KH * KW));
     }
-    if (rc == CAMEL_HIP_OK) {
-        GemmArgs g = conv_args(static_cast<const float *>(wt), static_cast<const float *>(xt), bias,
-                               y, N, C, H, W, Co, KH, KW, stride, pad, OH, OW, flags);
-        rc = run_gemm<T, LOAD_VEC, LOAD_NHWC>(g, 1, "conv2d_nhwc_kernel");
+    CAMEL_RETURN_IF(check_launch("nchw_to_nhwc_kernel"));
+    GemmArgs g = conv_args(wt.f(), x_nhwc ? x : xt.f(), bias, y, N, C, H, W, Co, KH, KW, stride, pad,
+                           OH, OW, flags);
+    if (pool) {
+        g.PW = (int)(OW / 2);
+        g.PP = (int)((OH / 2) * (OW / 2));
+        g.N = (int)(N * g.PP * 4);
+        CAMEL_RETURN_IF((run_gemm<T, LOAD_VEC, LOAD_NHWC_POOL>(g, 1, "conv2d_pool_kernel")));
+    } else {
+        CAMEL_RETURN_IF((run_gemm<T, LOAD_VEC, LOAD_NHWC>(g, 1, "conv2d_nhwc_kernel")));
     }
-    camel_hip_free(wt);
-    camel_hip_free(xt);
-    CAMEL_RETURN_IF(rc);
     return ok();
 }
 
@@ -1401,6 +1557,95 @@ int conv2d_gather(const float *x, const float *w, const float *bias, float *y, i
                   : run_gemm<TileGather, LOAD_SCALAR, LOAD_CONV>(g, 1, "conv2d_igemm_kernel");
     CAMEL_RETURN_IF(rc);
     return ok();
+}
+
+// Shared argument checks of the conv2d entry points.
+int conv_check(const float *x, const float *w, const float *bias, const float *y, int64_t N,
+               int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
+               int64_t pad, int flags, const char *what) {
+    const std::string name(what);
+    if (N < 0 || C <= 0 || H <= 0 || W <= 0 || Co <= 0 || KH <= 0 || KW <= 0 || stride <= 0 ||
+        pad < 0)
+        return fail(CAMEL_HIP_ERR_SHAPE, name + ": invalid geometry");
+    if (H + 2 * pad < KH || W + 2 * pad < KW)
+        return fail(CAMEL_HIP_ERR_SHAPE, name + ": kernel larger than padded input");
+    if (KH > 0xffff || KW > 0xffff) return fail(CAMEL_HIP_ERR_SHAPE, name + ": kernel too large");
+    const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    const int64_t K = C * KH * KW, P = OH * OW, NP = N * P;
+    if (N * C * H * W > INT32_MAX || NP > INT32_MAX || N * Co * P > INT32_MAX || Co * K > INT32_MAX)
+        return fail(CAMEL_HIP_ERR_SHAPE, name + ": tensor too large");
+    if (flags & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU | CAMEL_CONV_X_NHWC | CAMEL_CONV_Y_NHWC))
+        return fail(CAMEL_HIP_ERR_ARG, name + ": unknown flags");
+    if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, name + ": null bias");
+    if (N > 0 && (!x || !w || !y)) return fail(CAMEL_HIP_ERR_ARG, name + ": null operand");
+    return CAMEL_HIP_OK;
+}
+
+// Every conv2d runs here.  The NHWC implicit GEMM serves C % 16 == 0 and
+// reads an NHWC input in place; the direct kernel serves C*KH*KW <= 32 and
+// can write NHWC; every other layout combination goes through transposes
+// into pooled scratch, so all of them compute the same values.  pool: y is
+// the 2x2 stride-2 max pool of the result (from the GEMM epilogue when the
+// NHWC GEMM serves the shape, else a pool pass over a scratch result).
+int conv2d_run(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
+               int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+               int flags, bool pool) {
+    const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    const int64_t K = C * KH * KW, HW = H * W, P = OH * OW;
+    const bool x_nhwc = (flags & CAMEL_CONV_X_NHWC) != 0, y_nhwc = (flags & CAMEL_CONV_Y_NHWC) != 0;
+    const int epi = flags & (CAMEL_EPI_BIAS | CAMEL_EPI_RELU);
+    const bool aligned = (((uintptr_t)x | (uintptr_t)w) & 15) == 0;
+    // (the NCHW -> NHWC transpose runs one image per grid z, plus one z for
+    // the weights)
+    const bool gemm_nhwc = K > DIRECT_MAX_K && aligned && C % 16 == 0 && N < 65535;
+    auto nhwc_gemm = [&](float *out, bool pooled) -> int {
+        const bool k32 = C % 32 == 0;
+        if (Co > 64)
+            return k32 ? conv2d_nhwc<TileConv>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH,
+                                              OW, epi, x_nhwc, pooled)
+                       : conv2d_nhwc<TileConv16>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad,
+                                                OH, OW, epi, x_nhwc, pooled);
+        return k32 ? conv2d_nhwc<TileConv64>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH,
+                                            OW, epi, x_nhwc, pooled)
+                   : conv2d_nhwc<TileConv64k16>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad,
+                                               OH, OW, epi, x_nhwc, pooled);
+    };
+    if (pool) {
+        if (gemm_nhwc) return nhwc_gemm(y, true);
+        Scratch full;
+        CAMEL_RETURN_IF(full.alloc((size_t)(N * Co * P) * sizeof(float)));
+        CAMEL_RETURN_IF(conv2d_run(x, w, bias, full.f(), N, C, H, W, Co, KH, KW, stride, pad,
+                                   flags & ~CAMEL_CONV_Y_NHWC, false));
+        return camel_hip_maxpool2d(full.f(), y, N, Co, OH, OW, 2, 2, 2);
+    }
+    // NCHW result into y, or into scratch that is then transposed to NHWC.
+    const bool direct = K <= DIRECT_MAX_K;
+    const bool direct_nhwc_out = direct && y_nhwc && Co % 4 == 0 && ((uintptr_t)y & 15) == 0;
+    Scratch ytmp;
+    float *out = y;
+    if (y_nhwc && !direct_nhwc_out) {
+        CAMEL_RETURN_IF(ytmp.alloc((size_t)(N * Co * P) * sizeof(float)));
+        out = ytmp.f();
+    }
+    if (gemm_nhwc) {
+        CAMEL_RETURN_IF(nhwc_gemm(out, false));
+    } else {
+        Scratch xtmp;
+        const float *xs = x;
+        if (x_nhwc) {
+            CAMEL_RETURN_IF(xtmp.alloc((size_t)(N * C * HW) * sizeof(float)));
+            CAMEL_RETURN_IF(transpose_images(x, xtmp.f(), N, HW, C));
+            xs = xtmp.f();
+        }
+        if (direct)
+            CAMEL_RETURN_IF(conv2d_direct(xs, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH, OW,
+                                          epi, direct_nhwc_out));
+        else
+            CAMEL_RETURN_IF(conv2d_gather(xs, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH, OW,
+                                          epi));
+    }
+    if (out != y) CAMEL_RETURN_IF(transpose_images(out, y, N, Co, P));
+    return CAMEL_HIP_OK;
 }
 
 } // namespace
@@ -1464,6 +1709,27 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
     return ok();
 }
 
+int camel_hip_dense_softmax(const float *A, const float *B, const float *bias, float *C, int64_t M,
+                            int64_t N, int64_t K, int flags) {
+    if (M < 0 || N < 0 || K < 0) return fail(CAMEL_HIP_ERR_SHAPE, "dense_softmax: negative dimension");
+    if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
+        return fail(CAMEL_HIP_ERR_SHAPE, "dense_softmax: dimension too large");
+    if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, "dense_softmax: null bias");
+    if (M == 0 || N == 0) return ok();
+    if (!C || (K > 0 && (!A || !B))) return fail(CAMEL_HIP_ERR_ARG, "dense_softmax: null operand");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    if (thin_eligible(M, N, K)) {
+        CAMEL_RETURN_IF(launch_thin<true>(A, B, C, (int)M, (int)N, (int)K, bias, flags));
+        return ok();
+    }
+    // Unfused: the GEMM with its epilogue, then the row softmax in place
+    // (each row is read whole before it is written).
+    CAMEL_RETURN_IF(camel_hip_sgemm(A, B, C, M, N, K, bias, flags));
+    CAMEL_RETURN_IF(camel_hip_softmax_rows(C, C, M, N));
+    return ok();
+}
+
 int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int odt, void *C,
                              int64_t M, int64_t N, int64_t K) {
     if (!valid_dtype(adt) || !valid_dtype(bdt) || !valid_dtype(odt))
@@ -1482,38 +1748,28 @@ int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int
 int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y, int64_t N,
                      int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
                      int64_t stride, int64_t pad, int flags) {
-    if (N < 0 || C <= 0 || H <= 0 || W <= 0 || Co <= 0 || KH <= 0 || KW <= 0 || stride <= 0 ||
-        pad < 0)
-        return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: invalid geometry");
-    if (H + 2 * pad < KH || W + 2 * pad < KW)
-        return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: kernel larger than padded input");
-    if (KH > 0xffff || KW > 0xffff) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: kernel too large");
-    const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
-    const int64_t K = C * KH * KW, P = OH * OW, NP = N * P;
-    if (N * C * H * W > INT32_MAX || NP > INT32_MAX || N * Co * P > INT32_MAX || Co * K > INT32_MAX)
-        return fail(CAMEL_HIP_ERR_SHAPE, "conv2d: tensor too large");
-    if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, "conv2d: null bias");
+    CAMEL_RETURN_IF(conv_check(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, flags, "conv2d"));
     if (N == 0) return ok();
-    if (!x || !w || !y) return fail(CAMEL_HIP_ERR_ARG, "conv2d: null operand");
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
-    if (K <= DIRECT_MAX_K) return conv2d_direct(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
-                                                OW, flags);
-    const bool aligned = (((uintptr_t)x | (uintptr_t)w) & 15) == 0;
-    // The NHWC transpose runs one image per grid z (plus one z for the weights).
-    if (aligned && C % 16 == 0 && N < 65535) {
-        const bool k32 = C % 32 == 0;
-        if (Co > 64)
-            return k32 ? conv2d_nhwc<TileConv>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
-                                              OW, flags)
-                       : conv2d_nhwc<TileConv16>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad,
-                                                OH, OW, flags);
-        return k32 ? conv2d_nhwc<TileConv64>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH,
-                                            OW, flags)
-                   : conv2d_nhwc<TileConv64k16>(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad,
-                                               OH, OW, flags);
-    }
-    return conv2d_gather(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, OH, OW, flags);
+    CAMEL_RETURN_IF(conv2d_run(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, flags, false));
+    return ok();
+}
+
+int camel_hip_conv2d_pool2(const float *x, const float *w, const float *bias, float *y, int64_t N,
+                           int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
+                           int64_t stride, int64_t pad, int flags) {
+    CAMEL_RETURN_IF(
+        conv_check(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, flags, "conv2d_pool2"));
+    if (flags & CAMEL_CONV_Y_NHWC)
+        return fail(CAMEL_HIP_ERR_ARG, "conv2d_pool2: the pooled output is NCHW only");
+    const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    if (OH < 2 || OW < 2) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d_pool2: window larger than input");
+    if (N == 0) return ok();
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(conv2d_run(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, flags, true));
+    return ok();
 }
 
 } // extern "C"

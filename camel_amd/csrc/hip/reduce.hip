@@ -18,6 +18,7 @@
 // lower index on ties, which reproduces "first element, then strict '>'",
 // including the order of +0/-0; NaN never wins except as element 0.
 #include "common.h"
+#include "row_softmax.h"
 
 #include <cmath>
 
@@ -27,38 +28,6 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
-
-__device__ __forceinline__ double wave_sum(double s) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    return s;
-}
-
-// Row max with the reference's rule (first element, then strict '>'), value
-// only: NaNs never win unless the row starts with one.  Which of several
-// equal maxima wins cannot change the softmax (m is only used as m + 0.0,
-// which also maps -0.0 to +0.0), so no index is tracked.
-__device__ __forceinline__ float max_gt(float best, float v) { return v > best ? v : best; }
-
-__device__ __forceinline__ float wave_max_gt(float m) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = max_gt(m, __shfl_xor(m, off));
-    return m;
-}
-
-// e = exp(x - mb) rounded to fp32.  The device expf is within 1 ulp of the
-// reference's (float)std::exp((double)d); the softmax bar is rel-err 1e-6
-// (about 16 ulp), and fp32 exp keeps the kernel at HBM speed where the fp64
-// exp made it ALU-bound.
-__device__ __forceinline__ float softmax_exp(float v, float mb) { return expf(v - mb); }
-
-// y = fl32(e / s) bit-exactly, computed as fl32(e * fl64(1 / s)): the relative
-// error of the double product is <= 2^-52, while a quotient of two fp32 values
-// is never closer than 2^-49 (relative) to an fp32 rounding midpoint, so both
-// round to the same fp32 value.  This replaces a per-element fp32 division.
-__device__ __forceinline__ float softmax_div(float e, double rcp) {
-    return (float)((double)e * rcp);
-}
 
 // One wave per row, the whole row in registers: ITEMS float4 per lane (VEC,
 // cols % 4 == 0 and 16-byte aligned rows) or ITEMS*4 scalars per lane.  Slots

@@ -54,6 +54,10 @@ enum camel_hip_compare_op {
 
 /* Epilogue flags of the GEMM / conv entry points. */
 enum camel_hip_epilogue { CAMEL_EPI_NONE = 0, CAMEL_EPI_BIAS = 1, CAMEL_EPI_RELU = 2 };
+/* Layout bits of the conv2d flags, for a fused layer chain that keeps an
+ * intermediate in the layout its consumer reads: x given as [N, H, W, C],
+ * y written as [N, OH, OW, Co].  Either is only an addressing change. */
+enum camel_hip_conv_layout { CAMEL_CONV_X_NHWC = 0x100, CAMEL_CONV_Y_NHWC = 0x200 };
 
 /* ---- runtime ------------------------------------------------------------- */
 /* Selects the device and creates the stream and device-side error flag.
@@ -105,6 +109,14 @@ int camel_hip_arange(int64_t *out, int64_t start, int64_t step, int64_t count);
  * (test/run/nn/svm.cml:31), both fused in the GEMM epilogue. */
 int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
                     const float *bias, int flags);
+/* C[M,N] = softmax_rows(A . B (+bias) (relu)): the dense..softmax of a
+ * classifier layer (README.md:43, `dense<w3, b3>..softmax`; softmax as in
+ * test/run/nn/mnist.cml:13-25) fused into one pass when N <= 32 (each row's
+ * softmax runs on the GEMM's own wave); equals camel_hip_sgemm followed by
+ * camel_hip_softmax_rows.  No reference operator: the reference's compose
+ * (`..`, src/builtin/operators/macro.cpp:30) is a stub. */
+int camel_hip_dense_softmax(const float *A, const float *B, const float *bias, float *C, int64_t M,
+                            int64_t N, int64_t K, int flags);
 /* Mixed-dtype matmul through double (Int64 / Bool operands, promoted output
  * dtype, promoteTensorTypes runtime.cpp:570-580). */
 int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int odt, void *C,
@@ -112,10 +124,21 @@ int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int
 
 /* ---- conv2d / pooling (no reference op; defined by composition) --------- */
 /* y[N,Co,OH,OW] = conv(x[N,C,H,W], w[Co,C,KH,KW]) (+bias[Co]) (relu), NCHW,
- * implicit GEMM on the same MFMA core.  OH = (H+2*pad-KH)/stride+1. */
+ * implicit GEMM on the same MFMA core.  OH = (H+2*pad-KH)/stride+1.
+ * flags may add CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC (same values, other
+ * addressing). */
 int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y, int64_t N,
                      int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
                      int64_t stride, int64_t pad, int flags);
+/* y[N,Co,OH/2,OW/2] = maxpool2x2(conv2d(x) (+bias) (relu)), the
+ * conv2d_relu..maxpool2d of a CNN fused: the 2x2 stride-2 max (the rule of
+ * camel_hip_maxpool2d) is taken in the convolution's epilogue, so the
+ * full-size result never reaches HBM.  No reference operator (compose is a
+ * stub, src/builtin/operators/macro.cpp:30).  flags may add
+ * CAMEL_CONV_X_NHWC; OH, OW >= 2. */
+int camel_hip_conv2d_pool2(const float *x, const float *w, const float *bias, float *y, int64_t N,
+                           int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
+                           int64_t stride, int64_t pad, int flags);
 /* Max pool, NCHW, window KH x KW, first-then-strict-'>' rule of tensorMaxAxis
  * (runtime.cpp:953-958).  OH = (H-KH)/stride+1. */
 int camel_hip_maxpool2d(const float *x, float *y, int64_t N, int64_t C, int64_t H, int64_t W,

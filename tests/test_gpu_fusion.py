@@ -1,0 +1,265 @@
+"""Fused layer kernels (graph-level fusion of composed layers) against the
+unfused device chain and the CPU oracle.
+
+* dense..softmax (README.md:43 `dense<w3, b3>..softmax`): camel_hip_dense_softmax
+  equals camel_hip_sgemm then camel_hip_softmax_rows bit for bit where the
+  fused path serves (N <= 32, one value per lane), and the softmax of the
+  device GEMM result per the oracle.
+* conv2d layouts: CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC change addressing
+  only, so results equal the NCHW conv bit for bit.
+* conv2d..maxpool2d: camel_hip_conv2d_pool2 equals camel_hip_conv2d then
+  camel_hip_maxpool2d(2, 2, 2) bit for bit when both run one launch of the
+  same tile (every output then sums in the same order); the oracle bounds the
+  rest.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from camel_amd import _hip as H
+from camel_amd import datagen as D
+from oracle import ffi as O
+from tests import hipkit as K
+
+pytestmark = pytest.mark.gpu
+P = C.c_void_p
+F = np.float32
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _init():
+    H.call("camel_hip_init", 0)
+
+
+def _dense_softmax(x, w, b, flags):
+    M, Kd = x.shape
+    N = w.shape[1]
+    dx, dw, dy = K.dev(x), K.dev(w), K.empty(M * N * 4)
+    db = K.dev(b) if b is not None else None
+    H.call("camel_hip_dense_softmax", P(dx.ptr), P(dw.ptr), P(db.ptr) if db else None, P(dy.ptr),
+           M, N, Kd, flags)
+    return K.host(dy, F, (M, N))
+
+
+def _dense_then_softmax(x, w, b, flags):
+    M, Kd = x.shape
+    N = w.shape[1]
+    dx, dw, dh, dy = K.dev(x), K.dev(w), K.empty(M * N * 4), K.empty(M * N * 4)
+    db = K.dev(b) if b is not None else None
+    H.call("camel_hip_sgemm", P(dx.ptr), P(dw.ptr), P(dh.ptr), M, N, Kd, P(db.ptr) if db else None,
+           flags)
+    H.call("camel_hip_softmax_rows", P(dh.ptr), P(dy.ptr), M, N)
+    return K.host(dh, F, (M, N)), K.host(dy, F, (M, N))
+
+
+@pytest.mark.parametrize("M,N,Kd,flags", [
+    (1024, 10, 1024, H.EPI_BIAS),               # BASELINE config 2 classifier
+    (512, 10, 128, H.EPI_BIAS),                 # BASELINE config 5 classifier
+    (300, 7, 50, H.EPI_BIAS | H.EPI_RELU),      # relu before the softmax
+    (257, 32, 512, 0),                          # widest fused row, longest K for it
+    (200, 3, 1, H.EPI_BIAS),                    # K = 1
+])
+def test_dense_softmax_equals_unfused_chain(M, N, Kd, flags):
+    x = D.uniform(0x5100 + M, (M, Kd), -1.0, 1.0)
+    w = D.normal(0x5101 + N, (Kd, N), std=float(np.sqrt(1.0 / Kd)))
+    b = D.uniform(0x5102, (N,), -0.5, 0.5)
+    got = _dense_softmax(x, w, b, flags)
+    h, ref = _dense_then_softmax(x, w, b, flags)
+    np.testing.assert_array_equal(got, ref)
+    # and the softmax of the device dense result per the oracle (1e-6 relative)
+    p = O.softmax_rows(h)
+    assert np.max(np.abs(got - p) / np.maximum(p, 1e-30)) <= 1e-6
+    np.testing.assert_allclose(got.sum(axis=1, dtype=np.float64), 1.0, rtol=0, atol=1e-5)
+
+
+def test_dense_softmax_special_values_follow_the_softmax_rules():
+    # bias NaN in column 0: every row NaN (NaN wins only as element 0); +inf
+    # in another column: inf - inf = NaN there, the rest 0 -- the unfused
+    # kernel's rules, bit for bit.
+    x = D.uniform(0x5200, (96, 40), -1.0, 1.0)
+    w = D.normal(0x5201, (40, 9), std=0.2)
+    for col, val in ((0, np.nan), (4, np.inf), (2, -np.inf), (5, np.nan)):
+        b = D.uniform(0x5202, (9,), -0.5, 0.5)
+        b[col] = val
+        got = _dense_softmax(x, w, b, H.EPI_BIAS)
+        _, ref = _dense_then_softmax(x, w, b, H.EPI_BIAS)
+        np.testing.assert_array_equal(got, ref)
+
+
+def test_dense_softmax_wide_rows_take_the_unfused_path():
+    # N > 32: GEMM then the softmax kernel in place
+    x = D.uniform(0x5300, (64, 100), -1.0, 1.0)
+    w = D.normal(0x5301, (100, 70), std=0.1)
+    b = D.uniform(0x5302, (70,), -0.5, 0.5)
+    got = _dense_softmax(x, w, b, H.EPI_BIAS)
+    _, ref = _dense_then_softmax(x, w, b, H.EPI_BIAS)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_dense_softmax_argument_errors():
+    lib = H.load()
+    assert lib.camel_hip_dense_softmax(None, None, None, None, -1, 2, 2, 0) == H.ERR_SHAPE
+    assert lib.camel_hip_dense_softmax(None, None, None, None, 2, 2, 2, H.EPI_BIAS) == H.ERR_ARG
+    assert lib.camel_hip_dense_softmax(None, None, None, None, 0, 2, 2, 0) == 0
+
+
+# ------------------------------------------------------------------ conv2d layouts
+
+def _conv(x, w, b, geom, flags, pooled=False):
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    OH, OW = (H_ + 2 * pad - kh) // stride + 1, (W_ + 2 * pad - kw) // stride + 1
+    if pooled:
+        OH, OW = OH // 2, OW // 2
+    dx, dw = K.dev(x), K.dev(w)
+    db = K.dev(b) if b is not None else None
+    dy = K.empty(N * Co * OH * OW * 4)
+    H.call("camel_hip_conv2d_pool2" if pooled else "camel_hip_conv2d", P(dx.ptr), P(dw.ptr),
+           P(db.ptr) if db else None, P(dy.ptr), N, Cin, H_, W_, Co, kh, kw, stride, pad, flags)
+    return dy, (N, Co, OH, OW)
+
+
+GEOMS = [
+    (4, 1, 28, 28, 32, 3, 3, 1, 0),     # direct, K = 9 (CNN conv1), NHWC out in place
+    (2, 1, 13, 13, 6, 5, 5, 2, 0),      # direct, Co % 4 != 0: NHWC out through scratch
+    (3, 32, 26, 26, 64, 3, 3, 1, 0),    # NHWC implicit GEMM (CNN conv2)
+    (2, 16, 9, 11, 130, 3, 3, 2, 1),    # NHWC GEMM, 16-channel stages, Co > 128
+    (2, 12, 8, 8, 24, 3, 3, 1, 1),      # gather path (C % 16 != 0)
+]
+
+
+@pytest.mark.parametrize("geom", GEOMS)
+def test_conv2d_nhwc_layouts_change_addressing_only(geom):
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    x = D.normal(0x5400 + Cin, (N, Cin, H_, W_))
+    w = D.normal(0x5401 + Co, (Co, Cin, kh, kw)) * F(np.sqrt(2.0 / (kh * kw * Cin)))
+    b = D.uniform(0x5402, (Co,), -0.1, 0.1)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    dref, shape = _conv(x, w, b, geom, epi)
+    ref = K.host(dref, F, shape)
+    x_nhwc = np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+    dy, _ = _conv(x_nhwc, w, b, geom, epi | H.CONV_X_NHWC)
+    np.testing.assert_array_equal(K.host(dy, F, shape), ref)
+    dy, _ = _conv(x, w, b, geom, epi | H.CONV_Y_NHWC)
+    np.testing.assert_array_equal(K.host(dy, F, (shape[0], shape[2], shape[3], shape[1])),
+                                  ref.transpose(0, 2, 3, 1))
+    dy, _ = _conv(x_nhwc, w, b, geom, epi | H.CONV_X_NHWC | H.CONV_Y_NHWC)
+    np.testing.assert_array_equal(K.host(dy, F, (shape[0], shape[2], shape[3], shape[1])),
+                                  ref.transpose(0, 2, 3, 1))
+
+
+def test_conv2d_chain_in_nhwc_equals_nchw_chain():
+    # CNN conv1 (direct) writing NHWC straight into conv2 (NHWC GEMM) reading it
+    x = D.uniform(0x5500, (6, 1, 28, 28), 0.0, 1.0)
+    w1 = D.normal(0x5501, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
+    w2 = D.normal(0x5502, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288)))
+    b1, b2 = np.zeros(32, F), D.uniform(0x5503, (64,), -0.1, 0.1)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    h, _ = _conv(x, w1, b1, (6, 1, 28, 28, 32, 3, 3, 1, 0), epi)
+    y_ref, shape = _conv(K.host(h, F, (6, 32, 26, 26)), w2, b2, (6, 32, 26, 26, 64, 3, 3, 1, 0), epi)
+    h_nhwc, _ = _conv(x, w1, b1, (6, 1, 28, 28, 32, 3, 3, 1, 0), epi | H.CONV_Y_NHWC)
+    y, _ = _conv(K.host(h_nhwc, F, (6, 26, 26, 32)), w2, b2, (6, 32, 26, 26, 64, 3, 3, 1, 0),
+                 epi | H.CONV_X_NHWC)
+    np.testing.assert_array_equal(K.host(y, F, shape), K.host(y_ref, F, shape))
+
+
+def test_conv2d_unknown_flags_rejected():
+    lib = H.load()
+    x = K.empty(4 * 16 * 16 * 4)
+    rc = lib.camel_hip_conv2d(P(x.ptr), P(x.ptr), None, P(x.ptr), 1, 4, 4, 4, 4, 3, 3, 1, 0, 0x4000)
+    assert rc == H.ERR_ARG
+
+
+# ------------------------------------------------------------------ conv2d..maxpool2d
+
+POOL_GEOMS = [
+    (3, 32, 26, 26, 64, 3, 3, 1, 0),    # CNN conv2 + pool (24 -> 12)
+    (2, 32, 27, 25, 64, 3, 3, 1, 0),    # odd conv output (25 x 23): last row / column dropped
+    (2, 16, 12, 12, 130, 3, 3, 1, 1),   # 16-channel stages, Co > 128, pad 1
+    (2, 64, 9, 9, 96, 3, 3, 2, 1),      # stride 2 (5 x 5 -> 2 x 2)
+    (2, 1, 12, 12, 8, 3, 3, 1, 0),      # direct path: conv to scratch, then the pool kernel
+    (2, 12, 10, 10, 24, 3, 3, 1, 1),    # gather path: conv to scratch, then the pool kernel
+]
+
+
+@pytest.mark.parametrize("geom", POOL_GEOMS)
+def test_conv2d_pool2_equals_conv_then_maxpool(geom):
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    x = D.normal(0x5600 + Cin, (N, Cin, H_, W_))
+    w = D.normal(0x5601 + Co, (Co, Cin, kh, kw)) * F(np.sqrt(2.0 / (kh * kw * Cin)))
+    b = D.uniform(0x5602, (Co,), -0.1, 0.1)
+    for flags in (H.EPI_BIAS | H.EPI_RELU, 0):
+        bb = b if flags else None
+        dfull, shape = _conv(x, w, bb, geom, flags)
+        OH, OW = shape[2], shape[3]
+        dref = K.empty(N * Co * (OH // 2) * (OW // 2) * 4)
+        H.call("camel_hip_maxpool2d", P(dfull.ptr), P(dref.ptr), N, Co, OH, OW, 2, 2, 2)
+        dy, pshape = _conv(x, w, bb, geom, flags, pooled=True)
+        got = K.host(dy, F, pshape)
+        np.testing.assert_array_equal(got, K.host(dref, F, pshape))
+        # oracle: pool of the oracle conv, within the conv bound (max is 1-Lipschitz)
+        ref = O.maxpool2d(O.conv2d(x, w, bb, bool(flags), stride, pad), 2, 2)
+        K_ = Cin * kh * kw
+        mag = O.maxpool2d(O.conv2d(np.abs(x), np.abs(w), None, False, stride, pad), 2, 2)
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= 1e-5 * np.sqrt(K_) * mag + 1e-30)
+
+
+def test_conv2d_pool2_nan_windows_follow_the_pool_rule():
+    # NaN inputs reach some window positions; the fused epilogue keeps
+    # maxpool's order (first element, strict '>'), bit for bit.
+    geom = (2, 32, 14, 14, 64, 3, 3, 1, 1)
+    x = D.normal(0x5700, (2, 32, 14, 14))
+    x[0, 3, 5, 6] = np.nan
+    x[1, 0, 0, 0] = np.nan
+    x[1, 7, 13, 2] = -np.inf
+    w = D.normal(0x5701, (64, 32, 3, 3)) * F(0.08)
+    b = D.uniform(0x5702, (64,), -0.1, 0.1)
+    flags = H.EPI_BIAS | H.EPI_RELU
+    dfull, shape = _conv(x, w, b, geom, flags)
+    dref = K.empty(2 * 64 * 7 * 7 * 4)
+    H.call("camel_hip_maxpool2d", P(dfull.ptr), P(dref.ptr), 2, 64, 14, 14, 2, 2, 2)
+    dy, pshape = _conv(x, w, b, geom, flags, pooled=True)
+    got, ref = K.host(dy, F, pshape), K.host(dref, F, pshape)
+    assert np.isnan(ref).any()
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_conv2d_pool2_nhwc_input_and_errors():
+    geom = (3, 32, 26, 26, 64, 3, 3, 1, 0)
+    x = D.normal(0x5800, (3, 32, 26, 26))
+    w = D.normal(0x5801, (64, 32, 3, 3)) * F(0.08)
+    b = D.uniform(0x5802, (64,), -0.1, 0.1)
+    flags = H.EPI_BIAS | H.EPI_RELU
+    dy, pshape = _conv(x, w, b, geom, flags, pooled=True)
+    dy2, _ = _conv(np.ascontiguousarray(x.transpose(0, 2, 3, 1)), w, b, geom,
+                   flags | H.CONV_X_NHWC, pooled=True)
+    np.testing.assert_array_equal(K.host(dy2, F, pshape), K.host(dy, F, pshape))
+    lib = H.load()
+    d = K.empty(64)
+    assert lib.camel_hip_conv2d_pool2(P(d.ptr), P(d.ptr), None, P(d.ptr), 1, 1, 3, 3, 1, 3, 3, 1, 0,
+                                      0) == H.ERR_SHAPE
+    assert lib.camel_hip_conv2d_pool2(P(d.ptr), P(d.ptr), None, P(d.ptr), 1, 1, 8, 8, 1, 3, 3, 1, 0,
+                                      H.CONV_Y_NHWC) == H.ERR_ARG
+
+
+def test_conv2d_pool2_large_schedules_match_conv_then_pool():
+    # Enough tiles for whole rounds plus a partial round (column band or K
+    # split tail); schedule-dependent rounding stays within the conv bound.
+    for geom in ((64, 64, 56, 56, 128, 3, 3, 1, 1), (1, 16, 112, 130, 640, 3, 3, 1, 0)):
+        N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+        x = D.normal(0x5900 + Cin, (N, Cin, H_, W_))
+        w = D.normal(0x5901 + Co, (Co, Cin, kh, kw)) * F(np.sqrt(2.0 / (kh * kw * Cin)))
+        b = np.zeros(Co, F)
+        flags = H.EPI_BIAS | H.EPI_RELU
+        dfull, shape = _conv(x, w, b, geom, flags)
+        OH, OW = shape[2], shape[3]
+        dref = K.empty(N * Co * (OH // 2) * (OW // 2) * 4)
+        H.call("camel_hip_maxpool2d", P(dfull.ptr), P(dref.ptr), N, Co, OH, OW, 2, 2, 2)
+        dy, pshape = _conv(x, w, b, geom, flags, pooled=True)
+        got, ref = K.host(dy, F, pshape), K.host(dref, F, pshape)
+        mag = O.maxpool2d(O.conv2d_images(np.abs(x), np.abs(w), None, False, 0, 1, stride, pad), 2, 2)
+        diff = np.abs(got[:1].astype(np.float64) - ref[:1])
+        assert np.all(diff <= 2e-5 * np.sqrt(Cin * kh * kw) * mag + 1e-30)
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= 1e-3)
