@@ -168,8 +168,10 @@ def wl_skinny(steps, warmup):
     return {"ms": ms, "flop": flop, "bytes": nbytes}
 
 
-def wl_mlp(steps, warmup):
-    """dense 784->1024->1024->10 (+relu) then row softmax, batch 1024."""
+def wl_mlp(steps, warmup, fused=True):
+    """dense 784->1024->1024->10 (+relu) then row softmax, batch 1024.
+    fused: the classifier layer and the softmax run as one kernel
+    (camel_hip_dense_softmax); otherwise GEMM then the softmax kernel."""
     B = 1024
     dims = [784, 1024, 1024, 10]
     x = D.uniform(D.SEED_MLP, (B, dims[0]), 0.0, 1.0)
@@ -184,11 +186,15 @@ def wl_mlp(steps, warmup):
 
     def step():
         src = dx
-        for i in range(3):
+        for i in range(2 if fused else 3):
             flags = H.EPI_BIAS | (H.EPI_RELU if i < 2 else 0)
             sgemm_call(src, dws[i], acts[i], B, dims[i + 1], dims[i], dbs[i], flags)()
             src = acts[i]
-        H.call("camel_hip_softmax_rows", P(acts[2].ptr), P(dp.ptr), B, 10)
+        if fused:
+            H.call("camel_hip_dense_softmax", P(acts[1].ptr), P(dws[2].ptr), P(dbs[2].ptr), P(dp.ptr),
+                   B, 10, dims[2], H.EPI_BIAS)
+        else:
+            H.call("camel_hip_softmax_rows", P(acts[2].ptr), P(dp.ptr), B, 10)
 
     ms, wall = _time_loop(step, steps, warmup)
     flop = sum(2.0 * B * dims[i] * dims[i + 1] for i in range(3))
@@ -209,8 +215,11 @@ def wl_conv(steps, warmup):
     return {"ms": ms, "flop": flop, "x": x, "w": w, "b": b}
 
 
-def wl_cnn(steps, warmup):
-    """small CNN forward, batch 512 (valid 3x3 convs, 2x2 pool)."""
+def wl_cnn(steps, warmup, fused=True):
+    """small CNN forward, batch 512 (valid 3x3 convs, 2x2 pool).
+    fused: conv1 writes NHWC for conv2 to read in place, conv2 + relu + pool
+    are one kernel (camel_hip_conv2d_pool2), and dense2 + softmax one more
+    (camel_hip_dense_softmax); otherwise every layer is its own call."""
     B = 512
     x = D.uniform(D.SEED_CNN, (B, 1, 28, 28), 0.0, 1.0)
     w1 = D.normal(D.SEED_CNN + 1, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
@@ -229,6 +238,15 @@ def wl_cnn(steps, warmup):
     EPI = H.EPI_BIAS | H.EPI_RELU
 
     def step():
+        if fused:
+            H.call("camel_hip_conv2d", P(dx.ptr), P(d1.ptr), P(b1.ptr), P(a1.ptr), B, 1, 28, 28, 32,
+                   3, 3, 1, 0, EPI | H.CONV_Y_NHWC)
+            H.call("camel_hip_conv2d_pool2", P(a1.ptr), P(d2.ptr), P(b2.ptr), P(a3.ptr), B, 32, 26, 26,
+                   64, 3, 3, 1, 0, EPI | H.CONV_X_NHWC)
+            sgemm_call(a3, d3, a4, B, 128, 9216, b3, EPI)()
+            H.call("camel_hip_dense_softmax", P(a4.ptr), P(d4.ptr), P(b4.ptr), P(dp.ptr), B, 10, 128,
+                   H.EPI_BIAS)
+            return
         H.call("camel_hip_conv2d", P(dx.ptr), P(d1.ptr), P(b1.ptr), P(a1.ptr), B, 1, 28, 28, 32, 3, 3, 1, 0, EPI)
         H.call("camel_hip_conv2d", P(a1.ptr), P(d2.ptr), P(b2.ptr), P(a2.ptr), B, 32, 26, 26, 64, 3, 3, 1, 0, EPI)
         H.call("camel_hip_maxpool2d", P(a2.ptr), P(a3.ptr), B, 64, 24, 24, 2, 2, 2)
@@ -320,6 +338,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-suite", action="store_true", help="headline GEMM only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--unfused", action="store_true",
+                    help="mlp / cnn workloads: one call per layer (no fused kernels)")
     ap.add_argument("--workload", default="gemm4096",
                     choices=["gemm4096", "mlp", "conv2d", "cnn", "eltwise", "softmax", "skinny",
                              "copy"])
@@ -337,7 +357,8 @@ def main() -> int:
         # single-workload mode (used for profiling one kernel at a time)
         fn = {"mlp": wl_mlp, "conv2d": wl_conv, "cnn": wl_cnn, "eltwise": wl_eltwise,
               "softmax": wl_softmax, "skinny": wl_skinny, "copy": wl_copy}[args.workload]
-        res = fn(steps, warmup)
+        res = fn(steps, warmup, fused=False) if args.unfused and args.workload in ("mlp", "cnn") \
+            else fn(steps, warmup)
         keep = {k: v for k, v in res.items() if isinstance(v, (int, float, dict))}
         print(json.dumps({"workload": args.workload, **keep}))
         return 0
@@ -386,6 +407,11 @@ def main() -> int:
         suite["mlp_forward"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                 "unit": "GFLOP/s", "ms": round(r["ms"], 4),
                                 "roofline": roofline_mfma(r["flop"], r["ms"], _traffic("mlp"))}
+        r = wl_mlp(s_steps * 2, s_warm, fused=False)
+        suite["mlp_forward_unfused"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
+                                        "unit": "GFLOP/s", "ms": round(r["ms"], 4),
+                                        "note": "one call per layer, no fused kernels",
+                                        "roofline": roofline_mfma(r["flop"], r["ms"])}
         r = wl_conv(s_steps, s_warm)
         suite["conv2d_3x3"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                "unit": "GFLOP/s", "ms": round(r["ms"], 4),
@@ -394,6 +420,11 @@ def main() -> int:
         suite["cnn_forward"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                 "unit": "GFLOP/s", "ms": round(r["ms"], 4),
                                 "roofline": roofline_mfma(r["flop"], r["ms"], _traffic("cnn"))}
+        r = wl_cnn(s_steps, s_warm, fused=False)
+        suite["cnn_forward_unfused"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
+                                        "unit": "GFLOP/s", "ms": round(r["ms"], 4),
+                                        "note": "one call per layer, no fused kernels",
+                                        "roofline": roofline_mfma(r["flop"], r["ms"])}
         e = wl_eltwise(s_steps, s_warm)
         for name, r in e.items():
             suite[f"eltwise_{name}"] = {"value": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1),

@@ -106,6 +106,13 @@ struct GemmArgs {
     int PW, PP;
 };
 
+// Value of lane Q of this lane's quad (lanes 4i .. 4i+3): a DPP quad_perm
+// move, one VALU op with no LDS traffic.
+template <int Q> __device__ __forceinline__ float quad_lane(float v) {
+    constexpr int ctrl = Q | (Q << 2) | (Q << 4) | (Q << 6);
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xf, 0xf, false));
+}
+
 // LDS slot of B column n within a k-quad plane.  A 16-byte LDS access is
 // served 8 lanes at a time over the 32 banks; the register-transposed B
 // stores have lanes 4 columns apart (n = 4 nq + c), which would put 8 lanes
@@ -515,29 +522,96 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     // ---- epilogue ----
     const bool has_bias = (g.flags & CAMEL_EPI_BIAS) != 0 && g.partial == nullptr;
     const bool has_relu = (g.flags & CAMEL_EPI_RELU) != 0 && g.partial == nullptr;
-    if constexpr (BMODE == LOAD_NHWC_POOL) {
-        if (g.partial == nullptr) {
-            // A pool window is 4 consecutive columns, i.e. lanes r32 .. r32+3
-            // of one half-wave (window starts are multiples of 4).  Every lane
-            // takes part in the shuffles; the window's first lane stores the
-            // max in the order (0,0), (0,1), (1,0), (1,1) with a strict '>'
-            // (maxpool2x2_kernel's rule).  Rows and columns past the problem
-            // are uniform across a window.
+    // Bias values come into registers before the stores that follow them: as
+    // far as the compiler knows C may alias bias, so a bias load after a
+    // store waits for that store, one L2 round trip per element (measured:
+    // 18% of a K = 288 conv).  Per-row (conv) biases are loaded per row block
+    // i, 16 at a time; per-column (dense) biases once.
+    float bcol[T::FN];
+    if constexpr (!is_conv<BMODE>) {
 #pragma unroll
-            for (int j = 0; j < T::FN; ++j) {
-                const int col = n0 + wn * T::WTN + j * 32 + r32;
-                const int img = col / (4 * g.PP), win = (col - img * 4 * g.PP) >> 2;
-                const bool store_col = col < g.N && (r32 & 3) == 0;
+        for (int j = 0; j < T::FN; ++j) {
+            const int col = n0 + wn * T::WTN + j * 32 + r32;
+            bcol[j] = (has_bias && col < g.N) ? g.bias[col] : 0.f;
+        }
+    }
+    auto row_bias = [&](int i, float *brow) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm * T::WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            brow[v] = (has_bias && row < g.M) ? g.bias[row] : 0.f;
+        }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    // Calls body(bias_tag, relu_tag) with the epilogue flags as compile-time
+    // types, so the element loops carry no uniform branches.
+    auto with_flags = [&](auto body) {
+        if (has_bias && has_relu)
+            body(T_{}, T_{});
+        else if (has_bias)
+            body(T_{}, F_{});
+        else if (has_relu)
+            body(F_{}, T_{});
+        else
+            body(F_{}, F_{});
+    };
+    // Tiles inside M x N (most of them) store with no row / column guards.
+    const bool full_out = g.partial == nullptr && m0 + T::BM <= g.M && n0 + T::BN <= g.N;
+    if constexpr (BMODE == LOAD_NHWC_POOL) {
+        if (full_out) {
+            with_flags([&](auto bias_tag, auto relu_tag) {
 #pragma unroll
                 for (int i = 0; i < T::FM; ++i) {
+                    float brow[16];
+                    if constexpr (decltype(bias_tag)::value) row_bias(i, brow);
+#pragma unroll
+                    for (int j = 0; j < T::FN; ++j) {
+                        const int col = n0 + wn * T::WTN + j * 32 + r32;
+                        const int img = col / (4 * g.PP), win = (col - img * 4 * g.PP) >> 2;
+                        float *out = g.C + (size_t)img * g.M * g.PP + win;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int row = m0 + wm * T::WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                            float x = acc[i][j][v];
+                            if constexpr (decltype(bias_tag)::value) x = x + brow[v];
+                            if constexpr (decltype(relu_tag)::value) x = relu_idiom(x);
+                            const float x1 = quad_lane<1>(x), x2 = quad_lane<2>(x),
+                                        x3 = quad_lane<3>(x);
+                            float mx = x;
+                            if (x1 > mx) mx = x1;
+                            if (x2 > mx) mx = x2;
+                            if (x3 > mx) mx = x3;
+                            if ((r32 & 3) == 0) out[(size_t)row * g.PP] = mx;
+                        }
+                    }
+                }
+            });
+            return;
+        }
+        if (g.partial == nullptr) {
+            // A pool window is 4 consecutive columns, i.e. lanes r32 .. r32+3
+            // of one half-wave (window starts are multiples of 4), one DPP
+            // quad.  Every lane takes part in the moves; the window's first
+            // lane stores the max in the order (0,0), (0,1), (1,0), (1,1) with
+            // a strict '>' (maxpool2x2_kernel's rule).  Rows and columns past
+            // the problem are uniform across a window.
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i) {
+                float brow[16];
+                row_bias(i, brow);
+#pragma unroll
+                for (int j = 0; j < T::FN; ++j) {
+                    const int col = n0 + wn * T::WTN + j * 32 + r32;
+                    const int img = col / (4 * g.PP), win = (col - img * 4 * g.PP) >> 2;
+                    const bool store_col = col < g.N && (r32 & 3) == 0;
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int row = m0 + wm * T::WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
                         float x = acc[i][j][v];
-                        if (has_bias) x = x + (row < g.M ? g.bias[row] : 0.f);
+                        if (has_bias) x = x + brow[v];
                         if (has_relu) x = relu_idiom(x);
-                        const float x1 = __shfl_down(x, 1), x2 = __shfl_down(x, 2),
-                                    x3 = __shfl_down(x, 3);
+                        const float x1 = quad_lane<1>(x), x2 = quad_lane<2>(x), x3 = quad_lane<3>(x);
                         float mx = x;
                         if (x1 > mx) mx = x1;
                         if (x2 > mx) mx = x2;
@@ -550,18 +624,50 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             return;
         }
     }
+    if (full_out) {
+        with_flags([&](auto bias_tag, auto relu_tag) {
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) {
-        const int col = n0 + wn * T::WTN + j * 32 + r32;
-        if (col >= g.N) continue;
-        size_t col_off = col;
-        if constexpr (is_conv<BMODE>) {
-            const int img = col / g.P, p = col - img * g.P;
-            col_off = (size_t)img * g.M * g.P + p;
-        }
-        const float bias_col = (has_bias && !is_conv<BMODE>) ? g.bias[col] : 0.f;
+            for (int i = 0; i < T::FM; ++i) {
+                float brow[16];
+                if constexpr (is_conv<BMODE> && decltype(bias_tag)::value) row_bias(i, brow);
 #pragma unroll
-        for (int i = 0; i < T::FM; ++i) {
+                for (int j = 0; j < T::FN; ++j) {
+                    const int col = n0 + wn * T::WTN + j * 32 + r32;
+                    float *out;
+                    if constexpr (is_conv<BMODE>) {
+                        const int img = col / g.P, p = col - img * g.P;
+                        out = g.C + (size_t)img * g.M * g.P + p;
+                    } else {
+                        out = g.C + col;
+                    }
+                    const size_t row_stride = is_conv<BMODE> ? (size_t)g.P : (size_t)g.ldc;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int row = m0 + wm * T::WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                        float x = acc[i][j][v];
+                        if constexpr (decltype(bias_tag)::value)
+                            x = x + (is_conv<BMODE> ? brow[v] : bcol[j]);
+                        if constexpr (decltype(relu_tag)::value) x = relu_idiom(x);
+                        out[(size_t)row * row_stride] = x;
+                    }
+                }
+            }
+        });
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < T::FM; ++i) {
+        float brow[16];
+        if constexpr (is_conv<BMODE>) row_bias(i, brow);
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j) {
+            const int col = n0 + wn * T::WTN + j * 32 + r32;
+            if (col >= g.N) continue;
+            size_t col_off = col;
+            if constexpr (is_conv<BMODE>) {
+                const int img = col / g.P, p = col - img * g.P;
+                col_off = (size_t)img * g.M * g.P + p;
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int row = m0 + wm * T::WTM + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
@@ -572,7 +678,11 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                               (size_t)(row - m0) * T::BN + (col - n0)] = x;
                     continue;
                 }
-                if (has_bias) x = x + (is_conv<BMODE> ? g.bias[row] : bias_col);
+                if constexpr (is_conv<BMODE>) {
+                    if (has_bias) x = x + brow[v];
+                } else {
+                    if (has_bias) x = x + bcol[j];
+                }
                 if (has_relu) x = relu_idiom(x);
                 if constexpr (is_conv<BMODE>)
                     g.C[col_off + (size_t)row * g.P] = x;
@@ -1068,10 +1178,7 @@ constexpr int DIRECT_MAX_K = 32;
 // around a lone scalar load and its full latency).
 // PIX consecutive output pixels per thread (P % PIX == 0, so they share an
 // image): the channel loop then stores PIX-wide vectors.
-// YNHWC: y is [N][OH][OW][Co] (Co % 4 == 0, 16-byte aligned), for a consumer
-// that reads NHWC; channels go four at a time into one 16-byte store per
-// pixel, and every value is computed exactly as for the NCHW output.
-template <int KMAX, bool EXACT, int PIX, bool YNHWC = false>
+template <int KMAX, bool EXACT, int PIX>
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(
     const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
@@ -1110,30 +1217,6 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
     // Epilogue flags are fixed per variant so the channel loop has no
     // branches and its scalar loads batch across unrolled channels.
     auto channels = [&](auto has_bias, auto has_relu) {
-        if constexpr (YNHWC) {
-            float *yp = y + ((size_t)img * P + p) * Co;
-            for (int co = 0; co < Co; co += 4) {
-                float4 out[PIX];
-#pragma unroll
-                for (int c4 = 0; c4 < 4; ++c4) {
-                    const float *wr = w + (size_t)(co + c4) * K;
-#pragma unroll
-                    for (int j = 0; j < PIX; ++j) {
-                        float acc = 0.f;
-#pragma unroll
-                        for (int k = 0; k < KMAX; ++k)
-                            if (EXACT || k < K) acc = __builtin_fmaf(wr[k], xv[j][k], acc);
-                        if constexpr (decltype(has_bias)::value) acc = acc + bias[co + c4];
-                        if constexpr (decltype(has_relu)::value) acc = relu_idiom(acc);
-                        (c4 == 0 ? out[j].x : c4 == 1 ? out[j].y : c4 == 2 ? out[j].z : out[j].w) = acc;
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < PIX; ++j)
-                    *reinterpret_cast<float4 *>(yp + (size_t)j * Co + co) = out[j];
-            }
-            return;
-        }
 #pragma unroll 4
         for (int co = 0; co < Co; ++co) {
             const float *wr = w + (size_t)co * K;
@@ -1162,6 +1245,94 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
         channels(F_{}, T_{});
     else
         channels(F_{}, F_{});
+}
+
+// Direct convolution writing NHWC y [N][OH][OW][Co] (Co % 4 == 0, 16-byte
+// aligned), for a consumer that reads NHWC.  Thread = one output pixel of a
+// block's 256 consecutive pixels, channels as in conv2d_direct_kernel (the
+// same k-ascending fp32 FMA chain with wave-uniform weights through scalar
+// loads, bias, relu, so both layouts hold identical values), DN_CH channels
+// at a time through an LDS tile [pixel][channel]; the block then writes its
+// 256 pixel rows with 16-byte stores, which for Co <= DN_CH is one
+// contiguous run of 256 Co floats.  (Storing each thread's channels straight
+// to NHWC puts a wave's 16-byte stores 64 lines apart, and a thread per
+// (pixel, 4 channels) issues per-lane weight loads: both measured 3x slower
+// than the NCHW kernel.)
+constexpr int DN_PIX = 256, DN_CH = 32;
+
+template <int KMAX, bool EXACT, int CH = DN_CH>
+__global__ __launch_bounds__(DN_PIX) void conv2d_direct_nhwc_kernel(
+    const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
+    float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
+    int stride, int pad, int flags) {
+    constexpr int LD = CH + 1; // odd row stride: a wave's column writes hit distinct banks
+    __shared__ float tile[DN_PIX * LD];
+    const int K = C * KH * KW;
+    const int pg0 = blockIdx.x * DN_PIX, pg = pg0 + (int)threadIdx.x;
+    const int npix = min(DN_PIX, NP - pg0);
+    float xv[KMAX];
+    {
+        const int pc = pg < NP ? pg : NP - 1; // rows past the end compute a copy, never stored
+        const int img = pc / P, p = pc - img * P;
+        const int oh = p / OW, ow = p - oh * OW;
+        const int ih0 = oh * stride - pad, iw0 = ow * stride - pad;
+        const float *xi = x + (size_t)img * C * H * W;
+        int c = 0, kh = 0, kw = 0;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+            float v = 0.f;
+            if (EXACT || k < K) {
+                const int ih = ih0 + kh, iw = iw0 + kw;
+                if (ih >= 0 && ih < H && iw >= 0 && iw < W) v = xi[((size_t)c * H + ih) * W + iw];
+                if (++kw == KW) {
+                    kw = 0;
+                    if (++kh == KH) {
+                        kh = 0;
+                        ++c;
+                    }
+                }
+            }
+            xv[k] = v;
+        }
+    }
+    float *trow = tile + threadIdx.x * LD;
+    auto channels = [&](auto has_bias, auto has_relu, int c0, int cw) {
+#pragma unroll 4
+        for (int cc = 0; cc < cw; ++cc) {
+            const int co = c0 + cc;
+            const float *wr = w + (size_t)co * K;
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < KMAX; ++k)
+                if (EXACT || k < K) acc = __builtin_fmaf(wr[k], xv[k], acc);
+            if constexpr (decltype(has_bias)::value) acc = acc + bias[co];
+            if constexpr (decltype(has_relu)::value) acc = relu_idiom(acc);
+            trow[cc] = acc;
+        }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool b = (flags & CAMEL_EPI_BIAS) != 0, r = (flags & CAMEL_EPI_RELU) != 0;
+    for (int c0 = 0; c0 < Co; c0 += CH) {
+        const int cw = min(CH, Co - c0); // a multiple of 4
+        if (b && r)
+            channels(T_{}, T_{}, c0, cw);
+        else if (b)
+            channels(T_{}, F_{}, c0, cw);
+        else if (r)
+            channels(F_{}, T_{}, c0, cw);
+        else
+            channels(F_{}, F_{}, c0, cw);
+        __syncthreads();
+        const int q4 = cw >> 2;
+        for (int i = threadIdx.x; i < npix * q4; i += DN_PIX) {
+            const int row = i / q4, q = i - row * q4;
+            const float *t = tile + row * LD + 4 * q;
+            *reinterpret_cast<float4 *>(y + (size_t)(pg0 + row) * Co + c0 + 4 * q) =
+                make_float4(t[0], t[1], t[2], t[3]);
+        }
+        __syncthreads();
+    }
 }
 
 // ---- host-side launch -----------------------------------------------------------
@@ -1382,11 +1553,24 @@ int conv2d_direct(const float *x, const float *w, const float *bias, float *y, i
                   int64_t pad, int64_t OH, int64_t OW, int flags, bool y_nhwc) {
     const int64_t P = OH * OW, NP = N * P;
     const int64_t K = C * KH * KW;
+    if (y_nhwc) {
+        // Co % 4 == 0 and y 16-byte aligned (checked by the caller)
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3((unsigned)((NP + DN_PIX - 1) / DN_PIX)), dim3(DN_PIX), 0, stream(),
+                               x, w, bias, y, (int)NP, (int)P, (int)OW, (int)C, (int)H, (int)W,
+                               (int)Co, (int)KH, (int)KW, (int)stride, (int)pad, flags);
+            return check_launch("conv2d_direct_nhwc_kernel");
+        };
+        if (K == 9) return go(conv2d_direct_nhwc_kernel<9, true>);
+        if (K == 25) return go(conv2d_direct_nhwc_kernel<25, true>);
+        if (K == 27) return go(conv2d_direct_nhwc_kernel<27, true>);
+        if (K <= 16) return go(conv2d_direct_nhwc_kernel<16, false>);
+        return go(conv2d_direct_nhwc_kernel<DIRECT_MAX_K, false>);
+    }
     // 2 pixels per thread (8-byte stores) when every channel plane of y
     // stays 8-byte aligned (measured 2-4% faster than 1 or 4 at the CNN's
-    // first layer); 1 otherwise.  NHWC output (Co % 4 == 0, 16-byte aligned
-    // y) only needs the pixel pair inside one image.
-    const bool pair = P % 2 == 0 && (y_nhwc || ((uintptr_t)y & 7) == 0);
+    // first layer); 1 otherwise.
+    const bool pair = P % 2 == 0 && ((uintptr_t)y & 7) == 0;
     auto go = [&](auto kernel, int pix) {
         const int64_t threads = (NP + pix - 1) / pix;
         hipLaunchKernelGGL(kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream(), x,
@@ -1394,23 +1578,21 @@ int conv2d_direct(const float *x, const float *w, const float *bias, float *y, i
                            (int)KH, (int)KW, (int)stride, (int)pad, flags);
         return check_launch("conv2d_direct_kernel");
     };
-    auto pick = [&](auto ynhwc) -> int {
-        constexpr bool YN = decltype(ynhwc)::value;
-        // Exact kernels for the usual first layers: 3x3 and 5x5 over 1 or 3
-        // channels.
-        if (K == 9)
-            return pair ? go(conv2d_direct_kernel<9, true, 2, YN>, 2)
-                        : go(conv2d_direct_kernel<9, true, 1, YN>, 1);
-        if (K == 25)
-            return pair ? go(conv2d_direct_kernel<25, true, 2, YN>, 2)
-                        : go(conv2d_direct_kernel<25, true, 1, YN>, 1);
-        if (K == 27)
-            return pair ? go(conv2d_direct_kernel<27, true, 2, YN>, 2)
-                        : go(conv2d_direct_kernel<27, true, 1, YN>, 1);
-        if (K <= 16) return go(conv2d_direct_kernel<16, false, 1, YN>, 1);
-        return go(conv2d_direct_kernel<DIRECT_MAX_K, false, 1, YN>, 1);
-    };
-    CAMEL_RETURN_IF(y_nhwc ? pick(std::true_type{}) : pick(std::false_type{}));
+    // Exact kernels for the usual first layers: 3x3 and 5x5 over 1 or 3
+    // channels.
+    if (K == 9)
+        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<9, true, 2>, 2)
+                             : go(conv2d_direct_kernel<9, true, 1>, 1));
+    else if (K == 25)
+        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<25, true, 2>, 2)
+                             : go(conv2d_direct_kernel<25, true, 1>, 1));
+    else if (K == 27)
+        CAMEL_RETURN_IF(pair ? go(conv2d_direct_kernel<27, true, 2>, 2)
+                             : go(conv2d_direct_kernel<27, true, 1>, 1));
+    else if (K <= 16)
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<16, false, 1>, 1));
+    else
+        CAMEL_RETURN_IF(go(conv2d_direct_kernel<DIRECT_MAX_K, false, 1>, 1));
     return ok();
 }
 
