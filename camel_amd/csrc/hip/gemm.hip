@@ -1260,16 +1260,16 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
 // than the NCHW kernel.)
 constexpr int DN_PIX = 256, DN_CH = 32;
 
-template <int KMAX, bool EXACT, int CH = DN_CH>
-__global__ __launch_bounds__(DN_PIX) void conv2d_direct_nhwc_kernel(
+template <int KMAX, bool EXACT, int CH = DN_CH, int PIXB = DN_PIX>
+__global__ __launch_bounds__(PIXB) void conv2d_direct_nhwc_kernel(
     const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
     int stride, int pad, int flags) {
     constexpr int LD = CH + 1; // odd row stride: a wave's column writes hit distinct banks
-    __shared__ float tile[DN_PIX * LD];
+    __shared__ float tile[PIXB * LD];
     const int K = C * KH * KW;
-    const int pg0 = blockIdx.x * DN_PIX, pg = pg0 + (int)threadIdx.x;
-    const int npix = min(DN_PIX, NP - pg0);
+    const int pg0 = blockIdx.x * PIXB, pg = pg0 + (int)threadIdx.x;
+    const int npix = min(PIXB, NP - pg0);
     float xv[KMAX];
     {
         const int pc = pg < NP ? pg : NP - 1; // rows past the end compute a copy, never stored
@@ -1325,7 +1325,7 @@ __global__ __launch_bounds__(DN_PIX) void conv2d_direct_nhwc_kernel(
             channels(F_{}, F_{}, c0, cw);
         __syncthreads();
         const int q4 = cw >> 2;
-        for (int i = threadIdx.x; i < npix * q4; i += DN_PIX) {
+        for (int i = threadIdx.x; i < npix * q4; i += PIXB) {
             const int row = i / q4, q = i - row * q4;
             const float *t = tile + row * LD + 4 * q;
             *reinterpret_cast<float4 *>(y + (size_t)(pg0 + row) * Co + c0 + 4 * q) =

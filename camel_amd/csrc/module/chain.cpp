@@ -1,0 +1,284 @@
+// LayerChain: composed tensor layers applied in order, with adjacent layers
+// run as one fused kernel where that computes the same values (chain.h).
+#include "chain.h"
+
+#include "camel_hip.h"
+#include "runtime.h"
+
+#include <sstream>
+#include <stdexcept>
+
+namespace camel_amd::tensor {
+
+namespace {
+
+std::string stripPrefix(const std::string &name) {
+    return name.rfind("tensor:", 0) == 0 ? name.substr(7) : name;
+}
+
+// The NHWC implicit GEMM of libcamel_hip reads an NHWC input in place when
+// C % 16 == 0 and C*KH*KW exceeds the direct kernel's 32 (its transpose runs
+// one image per grid z, so the batch stays below 65535).  Only then is an
+// NHWC intermediate worth writing.
+bool readsNhwc(const LayerStep &conv, int64_t batch) {
+    const int64_t C = conv.w->dim(1), KH = conv.w->dim(2), KW = conv.w->dim(3);
+    return C % 16 == 0 && C * KH * KW > 32 && batch < 65535;
+}
+
+int64_t intOr(const LayerStep &s, size_t i, int64_t fallback) {
+    return i < s.ints.size() ? s.ints[i] : fallback;
+}
+
+// A device activation between two groups: a tensor, or an NHWC buffer of the
+// logical NCHW shape `shape` that only a conv reads.
+struct Activation {
+    const TensorObject *tensor = nullptr;
+    bool owned = false;
+    void *nhwc = nullptr;
+    std::vector<int64_t> shape;
+
+    Activation() = default;
+    Activation(const Activation &) = delete;
+    Activation &operator=(const Activation &) = delete;
+    Activation(Activation &&o) noexcept { *this = std::move(o); }
+    Activation &operator=(Activation &&o) noexcept {
+        if (this != &o) {
+            reset();
+            tensor = o.tensor;
+            owned = o.owned;
+            nhwc = o.nhwc;
+            shape = std::move(o.shape);
+            o.tensor = nullptr;
+            o.owned = false;
+            o.nhwc = nullptr;
+        }
+        return *this;
+    }
+    ~Activation() { reset(); }
+    void reset() {
+        if (owned && tensor) releaseTensor(const_cast<TensorObject *>(tensor));
+        if (nhwc) camel_hip_free(nhwc);
+        tensor = nullptr;
+        owned = false;
+        nhwc = nullptr;
+    }
+    static Activation of(TensorObject *t) {
+        Activation a;
+        a.tensor = t;
+        a.owned = true;
+        a.shape.assign(t->shape(), t->shape() + t->rank());
+        return a;
+    }
+};
+
+const TensorObject *requireLive(const TensorObject *t) {
+    if (t && !isLiveTensor(t)) throw std::invalid_argument("chain layer weights were released");
+    return t;
+}
+
+} // namespace
+
+void LayerChain::append(const std::string &name, std::vector<const TensorObject *> tensors,
+                        std::vector<int64_t> ints) {
+    const std::string op = stripPrefix(name);
+    LayerStep s{};
+    auto tensor = [&](size_t i) { return i < tensors.size() ? tensors[i] : nullptr; };
+    if (op == "dense" || op == "dense_relu") {
+        s.kind = LayerKind::Dense;
+        s.relu = op == "dense_relu";
+        if (!tensor(0)) throw std::invalid_argument("dense requires weights");
+    } else if (op == "conv2d" || op == "conv2d_relu") {
+        s.kind = LayerKind::Conv2d;
+        s.relu = op == "conv2d_relu";
+        if (!tensor(0)) throw std::invalid_argument("conv2d requires weights");
+        if (tensor(0)->rank() != 4)
+            throw std::invalid_argument("conv2d requires rank-4 NCHW input and rank-4 weights");
+    } else if (op == "relu") {
+        s.kind = LayerKind::Relu;
+    } else if (op == "softmax") {
+        s.kind = LayerKind::Softmax;
+    } else if (op == "maxpool2d") {
+        s.kind = LayerKind::MaxPool2d;
+    } else if (op == "reshape") {
+        s.kind = LayerKind::Reshape;
+    } else {
+        throw std::invalid_argument("Unrecognized layer operator: " + name);
+    }
+    s.w = tensor(0);
+    s.bias = tensor(1);
+    s.ints = std::move(ints);
+    steps_.push_back(std::move(s));
+}
+
+std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> shape) const {
+    std::vector<Group> groups;
+    // Batch of the current activation where it is known (rank-4 shapes are
+    // propagated through conv / pool / relu; anything else stops NHWC
+    // pairing, which only changes speed, never values).
+    int64_t batch = shape.size() == 4 ? shape[0] : -1;
+    const size_t n = steps_.size();
+    for (size_t i = 0; i < n;) {
+        const LayerStep &s = steps_[i];
+        Group g{};
+        g.step = &s;
+        size_t j = i + 1;
+        switch (s.kind) {
+        case LayerKind::Dense:
+            g.relu = s.relu;
+            if (!g.relu && j < n && steps_[j].kind == LayerKind::Relu) {
+                g.relu = true;
+                ++j;
+            }
+            g.kind = Group::Dense;
+            if (j < n && steps_[j].kind == LayerKind::Softmax) {
+                g.kind = Group::DenseSoftmax;
+                ++j;
+            }
+            batch = -1;
+            break;
+        case LayerKind::Conv2d:
+            g.kind = Group::Conv;
+            g.relu = s.relu;
+            if (!g.relu && j < n && steps_[j].kind == LayerKind::Relu) {
+                g.relu = true;
+                ++j;
+            }
+            if (j < n && steps_[j].kind == LayerKind::MaxPool2d && intOr(steps_[j], 0, 2) == 2 &&
+                intOr(steps_[j], 1, intOr(steps_[j], 0, 2)) == 2) {
+                g.pool = true;
+                ++j;
+            }
+            g.x_nhwc = !groups.empty() && groups.back().kind == Group::Conv && groups.back().y_nhwc;
+            g.y_nhwc = !g.pool && j < n && steps_[j].kind == LayerKind::Conv2d && batch >= 0 &&
+                       readsNhwc(steps_[j], batch);
+            break;
+        case LayerKind::Relu:
+            g.kind = Group::Relu;
+            break;
+        case LayerKind::Softmax:
+            g.kind = Group::Softmax;
+            batch = -1;
+            break;
+        case LayerKind::MaxPool2d:
+            g.kind = Group::MaxPool;
+            break;
+        case LayerKind::Reshape:
+            g.kind = Group::Reshape;
+            batch = s.ints.size() == 4 ? s.ints[0] : -1;
+            break;
+        }
+        groups.push_back(g);
+        i = j;
+    }
+    return groups;
+}
+
+std::string LayerChain::plan(std::span<const int64_t> shape) const {
+    std::ostringstream out;
+    for (const Group &g : schedule(shape)) {
+        const LayerStep &s = *g.step;
+        switch (g.kind) {
+        case Group::Dense:
+            out << (g.relu ? "dense_relu" : "dense");
+            break;
+        case Group::DenseSoftmax:
+            out << (g.relu ? "dense_relu+softmax" : "dense+softmax");
+            break;
+        case Group::Conv:
+            out << (g.relu ? "conv2d_relu" : "conv2d");
+            if (g.pool) out << "+maxpool2d(2,2)";
+            if (g.x_nhwc) out << " x=nhwc";
+            if (g.y_nhwc) out << " y=nhwc";
+            break;
+        case Group::Relu:
+            out << "relu";
+            break;
+        case Group::Softmax:
+            out << "softmax";
+            break;
+        case Group::MaxPool: {
+            const int64_t k = intOr(s, 0, 2);
+            out << "maxpool2d(" << k << "," << intOr(s, 1, k) << ")";
+            break;
+        }
+        case Group::Reshape:
+            out << "reshape";
+            break;
+        }
+        out << "\n";
+    }
+    return out.str();
+}
+
+TensorObject *LayerChain::apply(const TensorObject *x) const {
+    for (const LayerStep &s : steps_) {
+        requireLive(s.w);
+        requireLive(s.bias);
+    }
+    Activation cur;
+    cur.tensor = x;
+    cur.shape.assign(x->shape(), x->shape() + x->rank());
+    for (const Group &g : schedule(cur.shape)) {
+        const LayerStep &s = *g.step;
+        Activation next;
+        switch (g.kind) {
+        case Group::Dense:
+            next = Activation::of(tensorDense(cur.tensor, s.w, s.bias, g.relu));
+            break;
+        case Group::DenseSoftmax:
+            next = Activation::of(tensorDenseSoftmax(cur.tensor, s.w, s.bias, g.relu));
+            break;
+        case Group::Relu:
+            next = Activation::of(tensorRelu(cur.tensor));
+            break;
+        case Group::Softmax:
+            next = Activation::of(tensorSoftmax(cur.tensor));
+            break;
+        case Group::MaxPool: {
+            const int64_t k = intOr(s, 0, 2);
+            next = Activation::of(tensorMaxPool2d(cur.tensor, k, intOr(s, 1, k)));
+            break;
+        }
+        case Group::Reshape:
+            next = Activation::of(tensorReshape(cur.tensor, s.ints));
+            break;
+        case Group::Conv: {
+            const int64_t stride = intOr(s, 0, 1), pad = intOr(s, 1, 0);
+            const TypeCode xdt = cur.nhwc ? TypeCode::Float32 : cur.tensor->dtype();
+            auto os = conv2dOutputShape(cur.shape, xdt, s.w, s.bias, stride, pad);
+            if (g.pool) {
+                if (os[2] < 2 || os[3] < 2)
+                    throw std::invalid_argument("maxpool2d window larger than input");
+                os[2] /= 2;
+                os[3] /= 2;
+            }
+            const int64_t numel = os[0] * os[1] * os[2] * os[3];
+            void *y;
+            if (g.y_nhwc) {
+                next.shape.assign(os.begin(), os.end());
+                checkHip(camel_hip_malloc(&next.nhwc, (size_t)std::max<int64_t>(numel, 1) * 4));
+                y = next.nhwc;
+            } else {
+                next = Activation::of(TensorObject::create(TypeCode::Float32, os, Residence::Device));
+                y = numel > 0 ? const_cast<TensorObject *>(next.tensor)->deviceOutput() : nullptr;
+            }
+            if (numel > 0) {
+                const void *xin = cur.nhwc ? cur.nhwc : cur.tensor->deviceData();
+                const int layout = (g.x_nhwc ? CAMEL_CONV_X_NHWC : 0) | (g.y_nhwc ? CAMEL_CONV_Y_NHWC : 0);
+                conv2dLaunch(xin, cur.shape, s.w, s.bias, stride, pad, g.relu, g.pool, layout, y);
+            }
+            break;
+        }
+        }
+        cur = std::move(next);
+    }
+    if (cur.nhwc) throw std::logic_error("chain ended on an NHWC intermediate");
+    if (!cur.owned) {
+        // an empty chain: x -> x is a new tensor with the same payload
+        return tensorReshape(cur.tensor, cur.shape);
+    }
+    cur.owned = false;
+    return const_cast<TensorObject *>(cur.tensor);
+}
+
+} // namespace camel_amd::tensor

@@ -5,12 +5,15 @@
 // call op(with, norm, ctx), store the result slot).
 #include "camel_tensor.h"
 
+#include "chain.h"
 #include "operators.h"
 #include "runtime.h"
 
 #include <algorithm>
+#include <memory>
 #include <mutex>
 #include <sstream>
+#include <unordered_map>
 
 using namespace camel_amd;
 using namespace camel_amd::tensor;
@@ -70,6 +73,16 @@ bool buildView(int64_t n, const camel_value *values, VectorArgsView &view, std::
         view.push(code, values[i].slot);
     }
     return true;
+}
+
+// Live chains by handle (the address of the chain object).
+std::mutex g_chain_mutex;
+std::unordered_map<uint64_t, std::unique_ptr<LayerChain>> g_chains;
+
+LayerChain *chainOf(uint64_t handle) {
+    std::lock_guard<std::mutex> lock(g_chain_mutex);
+    auto it = g_chains.find(handle);
+    return it == g_chains.end() ? nullptr : it->second.get();
 }
 
 template <typename Fn> int guarded(Fn &&fn) {
@@ -291,6 +304,92 @@ int camel_tensor_resolve(const char *group, int64_t n_with, const uint32_t *with
     }
     if (!found) return fail(CAMEL_TENSOR_ERR_URI, "Unknown operator group: " + std::string(group));
     return fail(CAMEL_TENSOR_ERR_RESOLVE, "no overload of " + std::string(group) + " accepts these argument types");
+}
+
+int camel_chain_create(uint64_t *chain) {
+    if (!chain) return fail(CAMEL_TENSOR_ERR_ARG, "camel_chain_create: null handle");
+    auto c = std::make_unique<LayerChain>();
+    const uint64_t h = reinterpret_cast<uint64_t>(c.get());
+    std::lock_guard<std::mutex> lock(g_chain_mutex);
+    g_chains.emplace(h, std::move(c));
+    *chain = h;
+    return ok();
+}
+
+int camel_chain_append(uint64_t chain, const char *uri, int64_t n_with, const camel_value *with) {
+    LayerChain *c = chainOf(chain);
+    if (!c || !uri || n_with < 0 || (n_with > 0 && !with))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_chain_append: bad arguments");
+    // Bind arguments as LayerOperands reads them: tensors (Void for "no
+    // bias") first, then integers (an Array of integers counts as its items).
+    std::vector<const TensorObject *> tensors;
+    std::vector<int64_t> ints;
+    int64_t i = 0;
+    for (; i < n_with; ++i) {
+        const TypeCode code = static_cast<TypeCode>(with[i].code);
+        if (code == TypeCode::Void) {
+            tensors.push_back(nullptr);
+        } else if (code == TypeCode::Tensor) {
+            TensorObject *t = tensorOf(with[i].slot);
+            if (!t) return fail(CAMEL_TENSOR_ERR_ARG, "argument " + std::to_string(i) + " is not a live tensor handle");
+            tensors.push_back(t);
+        } else {
+            break;
+        }
+    }
+    for (; i < n_with; ++i) {
+        const TypeCode code = static_cast<TypeCode>(with[i].code);
+        if (code == TypeCode::Int32) {
+            ints.push_back(static_cast<int32_t>(static_cast<uint32_t>(with[i].slot)));
+        } else if (code == TypeCode::Int64) {
+            ints.push_back(static_cast<int64_t>(with[i].slot));
+        } else if (code == TypeCode::Array) {
+            ArrayObject *a = arrayOf(with[i].slot);
+            if (!a) return fail(CAMEL_TENSOR_ERR_ARG, "argument " + std::to_string(i) + " is not a live array handle");
+            return guarded([&] {
+                for (int64_t d : parseShapeArray(a, TypeCode::Array)) ints.push_back(d);
+                c->append(uri, tensors, ints);
+                return ok();
+            });
+        } else {
+            return fail(CAMEL_TENSOR_ERR_RUNTIME, "Expected integer argument");
+        }
+    }
+    return guarded([&] {
+        c->append(uri, tensors, ints);
+        return ok();
+    });
+}
+
+int camel_chain_apply(uint64_t chain, uint64_t x, uint64_t *result) {
+    LayerChain *c = chainOf(chain);
+    TensorObject *t = tensorOf(x);
+    if (!c || !t || !result) return fail(CAMEL_TENSOR_ERR_ARG, "camel_chain_apply: bad arguments");
+    return guarded([&] {
+        *result = toSlot(c->apply(t));
+        return ok();
+    });
+}
+
+int camel_chain_plan(uint64_t chain, int64_t rank, const int64_t *shape, char *buf, size_t cap,
+                     size_t *needed) {
+    LayerChain *c = chainOf(chain);
+    if (!c || rank < 0 || (rank > 0 && !shape))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_chain_plan: bad arguments");
+    const std::string text = c->plan(std::span<const int64_t>(shape, (size_t)rank));
+    if (needed) *needed = text.size() + 1;
+    if (buf && cap > 0) {
+        const size_t n = std::min(cap - 1, text.size());
+        std::memcpy(buf, text.data(), n);
+        buf[n] = '\0';
+    }
+    return ok();
+}
+
+int camel_chain_release(uint64_t chain) {
+    std::lock_guard<std::mutex> lock(g_chain_mutex);
+    if (g_chains.erase(chain) == 0) return fail(CAMEL_TENSOR_ERR_ARG, "camel_chain_release: not a live chain");
+    return ok();
 }
 
 int64_t camel_tensor_op_count(void) { return (int64_t)opNames().size(); }

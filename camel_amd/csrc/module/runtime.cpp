@@ -7,6 +7,7 @@
 
 #include "camel_hip.h"
 
+#include <array>
 #include <random>
 
 namespace camel_amd::tensor {
@@ -450,33 +451,94 @@ TensorObject *tensorDense(const TensorObject *x, const TensorObject *w, const Te
     return out;
 }
 
+// dense (relu) then row softmax, the classifier head of README.md:43.  Float32
+// runs camel_hip_dense_softmax (one fused kernel for N <= 32, otherwise the
+// GEMM then the softmax kernel: the values of tensorDense then
+// tensorSoftmax); other dtypes run those two functions.
+TensorObject *tensorDenseSoftmax(const TensorObject *x, const TensorObject *w,
+                                 const TensorObject *bias, bool relu) {
+    if (x->rank() != 2 || w->rank() != 2)
+        throw std::invalid_argument("dense currently only supports rank-2 tensors");
+    if (x->dim(1) != w->dim(0)) throw std::invalid_argument("dense dimension mismatch");
+    const int64_t M = x->dim(0), K = x->dim(1), N = w->dim(1);
+    if (bias && !(bias->numel() == static_cast<uint64_t>(N) &&
+                  (bias->rank() == 1 || (bias->rank() == 2 && bias->dim(0) == 1))))
+        throw std::invalid_argument("dense bias must have shape [N] or [1, N]");
+    const bool fp32 = x->dtype() == TypeCode::Float32 && w->dtype() == TypeCode::Float32 &&
+                      (!bias || bias->dtype() == TypeCode::Float32);
+    if (!fp32 || K == 0) {
+        TensorObject *y = tensorDense(x, w, bias, relu);
+        TensorObject *p = tensorSoftmax(y);
+        releaseTensor(y);
+        return p;
+    }
+    int64_t shape[] = {M, N};
+    TensorObject *out = deviceTensor(TypeCode::Float32, shape);
+    if (M == 0 || N == 0) return out;
+    const int flags = (bias ? CAMEL_EPI_BIAS : 0) | (relu ? CAMEL_EPI_RELU : 0);
+    checkHip(camel_hip_dense_softmax(static_cast<const float *>(x->deviceData()),
+                                     static_cast<const float *>(w->deviceData()),
+                                     bias ? static_cast<const float *>(bias->deviceData()) : nullptr,
+                                     static_cast<float *>(out->deviceOutput()), M, N, K, flags));
+    return out;
+}
+
 // conv2d: x [N, C, H, W], w [Co, C, KH, KW], bias [Co] -> y [N, Co, OH, OW],
 // OH = (H + 2 pad - KH) / stride + 1.  Float32 only.
-TensorObject *tensorConv2d(const TensorObject *x, const TensorObject *w, const TensorObject *bias,
-                           int64_t stride, int64_t pad, bool relu) {
-    if (x->rank() != 4 || w->rank() != 4)
+std::array<int64_t, 4> conv2dOutputShape(std::span<const int64_t> xs, TypeCode xdtype,
+                                         const TensorObject *w, const TensorObject *bias,
+                                         int64_t stride, int64_t pad) {
+    if (xs.size() != 4 || w->rank() != 4)
         throw std::invalid_argument("conv2d requires rank-4 NCHW input and rank-4 weights");
-    if (x->dtype() != TypeCode::Float32 || w->dtype() != TypeCode::Float32 ||
+    if (xdtype != TypeCode::Float32 || w->dtype() != TypeCode::Float32 ||
         (bias && bias->dtype() != TypeCode::Float32))
         throw std::invalid_argument("conv2d requires Float32 tensors");
-    if (x->dim(1) != w->dim(1)) throw std::invalid_argument("conv2d channel mismatch");
+    if (xs[1] != w->dim(1)) throw std::invalid_argument("conv2d channel mismatch");
     if (stride <= 0 || pad < 0) throw std::invalid_argument("conv2d stride must be positive and pad non-negative");
-    const int64_t N = x->dim(0), C = x->dim(1), H = x->dim(2), W = x->dim(3);
+    const int64_t H = xs[2], W = xs[3];
     const int64_t Co = w->dim(0), KH = w->dim(2), KW = w->dim(3);
     if (bias && bias->numel() != static_cast<uint64_t>(Co))
         throw std::invalid_argument("conv2d bias must have one value per output channel");
     if (H + 2 * pad < KH || W + 2 * pad < KW)
         throw std::invalid_argument("conv2d kernel larger than padded input");
-    int64_t shape[] = {N, Co, (H + 2 * pad - KH) / stride + 1, (W + 2 * pad - KW) / stride + 1};
+    return {xs[0], Co, (H + 2 * pad - KH) / stride + 1, (W + 2 * pad - KW) / stride + 1};
+}
+
+void conv2dLaunch(const void *x, std::span<const int64_t> xs, const TensorObject *w,
+                  const TensorObject *bias, int64_t stride, int64_t pad, bool relu, bool pool,
+                  int layout, void *y) {
+    const int64_t C = xs[1], KH = w->dim(2), KW = w->dim(3);
+    if (C == 0 || KH == 0 || KW == 0) throw std::invalid_argument("conv2d requires a non-empty kernel");
+    const int flags = (bias ? CAMEL_EPI_BIAS : 0) | (relu ? CAMEL_EPI_RELU : 0) | layout;
+    const float *b = bias ? static_cast<const float *>(bias->deviceData()) : nullptr;
+    auto *fn = pool ? camel_hip_conv2d_pool2 : camel_hip_conv2d;
+    checkHip(fn(static_cast<const float *>(x), static_cast<const float *>(w->deviceData()), b,
+                static_cast<float *>(y), xs[0], C, xs[2], xs[3], w->dim(0), KH, KW, stride, pad,
+                flags));
+}
+
+TensorObject *tensorConv2d(const TensorObject *x, const TensorObject *w, const TensorObject *bias,
+                           int64_t stride, int64_t pad, bool relu) {
+    const auto shape = conv2dOutputShape(shapeOf(x), x->dtype(), w, bias, stride, pad);
     TensorObject *out = deviceTensor(TypeCode::Float32, shape);
     if (out->numel() == 0) return out;
-    if (C == 0 || KH == 0 || KW == 0) throw std::invalid_argument("conv2d requires a non-empty kernel");
-    const int flags = (bias ? CAMEL_EPI_BIAS : 0) | (relu ? CAMEL_EPI_RELU : 0);
-    checkHip(camel_hip_conv2d(static_cast<const float *>(x->deviceData()),
-                              static_cast<const float *>(w->deviceData()),
-                              bias ? static_cast<const float *>(bias->deviceData()) : nullptr,
-                              static_cast<float *>(out->deviceOutput()), N, C, H, W, Co, KH, KW,
-                              stride, pad, flags));
+    conv2dLaunch(x->deviceData(), shapeOf(x), w, bias, stride, pad, relu, false, 0,
+                 out->deviceOutput());
+    return out;
+}
+
+// conv2d (+bias)(relu) then maxpool2d(2, 2): one fused kernel when the
+// convolution runs as the NHWC implicit GEMM (the pool max is taken in its
+// epilogue), else the convolution into scratch and the pool kernel.
+TensorObject *tensorConv2dPool2(const TensorObject *x, const TensorObject *w,
+                                const TensorObject *bias, int64_t stride, int64_t pad, bool relu) {
+    const auto cs = conv2dOutputShape(shapeOf(x), x->dtype(), w, bias, stride, pad);
+    if (cs[2] < 2 || cs[3] < 2) throw std::invalid_argument("maxpool2d window larger than input");
+    int64_t shape[] = {cs[0], cs[1], cs[2] / 2, cs[3] / 2};
+    TensorObject *out = deviceTensor(TypeCode::Float32, shape);
+    if (out->numel() == 0) return out;
+    conv2dLaunch(x->deviceData(), shapeOf(x), w, bias, stride, pad, relu, true, 0,
+                 out->deviceOutput());
     return out;
 }
 

@@ -7,6 +7,8 @@
 
 #include "tensor_object.h"
 
+#include <array>
+
 namespace camel_amd::tensor {
 
 TensorObject *tensorEmpty(TypeCode dtype, std::span<const int64_t> shape);
@@ -53,5 +55,25 @@ TensorObject *tensorDense(const TensorObject *x, const TensorObject *w, const Te
 TensorObject *tensorConv2d(const TensorObject *x, const TensorObject *w, const TensorObject *bias,
                            int64_t stride, int64_t pad, bool relu);
 TensorObject *tensorMaxPool2d(const TensorObject *x, int64_t kernel, int64_t stride);
+
+// Fused layer pairs for composed chains (the reference's compose `..` is a
+// stub, src/builtin/operators/macro.cpp:30): dense (relu) then softmax, and
+// conv2d (relu) then maxpool2d(2, 2).  Same checks and error texts as the
+// layers they fuse.
+TensorObject *tensorDenseSoftmax(const TensorObject *x, const TensorObject *w,
+                                 const TensorObject *bias, bool relu);
+TensorObject *tensorConv2dPool2(const TensorObject *x, const TensorObject *w,
+                                const TensorObject *bias, int64_t stride, int64_t pad, bool relu);
+// The conv2d checks (error texts of tensorConv2d) on an input of shape xs and
+// dtype xdtype; returns the NCHW output shape.
+std::array<int64_t, 4> conv2dOutputShape(std::span<const int64_t> xs, TypeCode xdtype,
+                                         const TensorObject *w, const TensorObject *bias,
+                                         int64_t stride, int64_t pad);
+// Runs a checked conv2d on device memory: x and y are NCHW unless `layout`
+// carries CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC; pool adds maxpool2d(2, 2)
+// (y is then the pooled NCHW result).
+void conv2dLaunch(const void *x, std::span<const int64_t> xs, const TensorObject *w,
+                  const TensorObject *bias, int64_t stride, int64_t pad, bool relu, bool pool,
+                  int layout, void *y);
 
 } // namespace camel_amd::tensor

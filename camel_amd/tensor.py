@@ -96,6 +96,12 @@ _SIG = {
     "camel_tensor_group_name": ([_I64], C.c_char_p),
     "camel_tensor_to_dlpack": ([_U64, C.c_int, C.POINTER(C.POINTER(DLManagedTensor))], C.c_int),
     "camel_tensor_from_dlpack": ([C.POINTER(DLManagedTensor), C.POINTER(_U64)], C.c_int),
+    "camel_chain_create": ([C.POINTER(_U64)], C.c_int),
+    "camel_chain_append": ([_U64, C.c_char_p, _I64, C.POINTER(Value)], C.c_int),
+    "camel_chain_apply": ([_U64, _U64, C.POINTER(_U64)], C.c_int),
+    "camel_chain_plan": ([_U64, _I64, C.POINTER(_I64), C.c_char_p, C.c_size_t,
+                          C.POINTER(C.c_size_t)], C.c_int),
+    "camel_chain_release": ([_U64], C.c_int),
 }
 
 # PyCapsule plumbing of the DLPack Python protocol: a capsule named
@@ -402,3 +408,46 @@ def live_count() -> int:
 
 def release_all() -> int:
     return int(load().camel_tensor_release_all())
+
+
+class Chain:
+    """A composed layer chain, `dense<w1, b1>..relu..softmax` (README.md:40-46):
+    layers appended with their bind arguments, then applied to a tensor
+    (`x->chain`).  Adjacent layers run as one fused kernel where that computes
+    the same values."""
+
+    def __init__(self, *layers):
+        h = _U64()
+        _check(load().camel_chain_create(C.byref(h)))
+        self.handle = h.value
+        for layer in layers:
+            if isinstance(layer, str):
+                self.append(layer)
+            else:
+                self.append(layer[0], *layer[1:])
+
+    def append(self, uri: str, *with_) -> "Chain":
+        keep: list = []
+        wv = [to_value(x, keep) for x in with_]
+        wa = (Value * max(len(wv), 1))(*wv)
+        _check(load().camel_chain_append(self.handle, uri.encode(), len(wv), wa))
+        return self
+
+    def __call__(self, x: "Tensor") -> "Tensor":
+        out = _U64()
+        _check(load().camel_chain_apply(self.handle, x.handle, C.byref(out)))
+        return Tensor(out.value)
+
+    def plan(self, shape) -> list[str]:
+        dims = (_I64 * max(len(shape), 1))(*shape)
+        need = C.c_size_t()
+        L = load()
+        _check(L.camel_chain_plan(self.handle, len(shape), dims, None, 0, C.byref(need)))
+        buf = C.create_string_buffer(need.value)
+        _check(L.camel_chain_plan(self.handle, len(shape), dims, buf, need.value, None))
+        return [line for line in buf.value.decode().split("\n") if line]
+
+    def release(self) -> None:
+        if self.handle:
+            _check(load().camel_chain_release(self.handle))
+            self.handle = 0

@@ -129,6 +129,31 @@ const char *camel_tensor_op_name(int64_t index);
 int64_t camel_tensor_group_count(void);
 const char *camel_tensor_group_name(int64_t index);
 
+/* ---- composed layer chains --------------------------------------------- */
+/* A chain is what `dense<w1, b1>..relu..dense<w2, b2>..softmax` denotes
+ * (README.md:40-46): layer operators with their bind arguments, applied in
+ * order; `x->chain` is camel_chain_apply.  The reference's compose operator
+ * `..` is a stub (src/builtin/operators/macro.cpp:30): this is the object a
+ * compose over this module's layer operators builds.  Apply runs adjacent
+ * layers as one fused kernel where that computes the same values (dense +
+ * relu, dense + softmax, conv2d + relu, conv2d + maxpool2d(2, 2), and a
+ * conv2d feeding a conv2d through an NHWC intermediate). */
+int camel_chain_create(uint64_t *chain);
+/* Appends a layer: uri "dense", "dense_relu", "relu", "softmax", "conv2d",
+ * "conv2d_relu", "maxpool2d" or "reshape" ("tensor:" prefix optional) with
+ * its bind arguments as the operator takes them: tensors (weights, then
+ * bias; Void for none), then integers (conv2d stride, pad; maxpool2d kernel,
+ * stride; reshape the shape, as integers or one Array).  Weights are
+ * borrowed: they must stay live while the chain is applied. */
+int camel_chain_append(uint64_t chain, const char *uri, int64_t n_with, const camel_value *with);
+/* x -> chain: a new tensor handle.  Errors carry the failing layer's text. */
+int camel_chain_apply(uint64_t chain, uint64_t x, uint64_t *result);
+/* The kernel groups apply would run for an input of this shape, one per line
+ * (e.g. "conv2d_relu+maxpool2d(2,2) x=nhwc"), NUL-terminated into buf. */
+int camel_chain_plan(uint64_t chain, int64_t rank, const int64_t *shape, char *buf, size_t cap,
+                     size_t *needed);
+int camel_chain_release(uint64_t chain);
+
 /* Plugin ABI version the reference's loader checks (dynamic.h:29). */
 int camel_tensor_abi_version(void);
 

@@ -1,0 +1,102 @@
+"""Composed layer chains (the object a compose `..` over tensor layers builds;
+the reference's compose is a stub, src/builtin/operators/macro.cpp:30): the
+fusion plan and the argument checks, on the CPU.  Planning reads only shapes,
+so no device is needed; tests/test_gpu_chain.py runs the chains."""
+import numpy as np
+import pytest
+
+from camel_amd import tensor as T
+
+F = np.float32
+
+
+@pytest.fixture(autouse=True)
+def _release():
+    yield
+    T.release_all()
+
+
+def z(*shape):
+    return T.Tensor.from_numpy(np.zeros(shape, F))
+
+
+def cnn_chain(c1=1, c2=32, c3=64):
+    return T.Chain(("conv2d", z(c2, c1, 3, 3), z(c2)), "relu",
+                   ("conv2d_relu", z(c3, c2, 3, 3), z(c3)), ("maxpool2d", 2, 2),
+                   ("reshape", 512, c3 * 144), ("dense_relu", z(c3 * 144, 128), z(128)),
+                   ("dense", z(128, 10), z(10)), "softmax")
+
+
+def test_cnn_chain_plan_fuses_every_pair():
+    # BASELINE config 5 as a chain: conv1 writes NHWC for conv2, conv2 + relu
+    # + pool are one kernel, the classifier and the softmax one more.
+    assert cnn_chain().plan((512, 1, 28, 28)) == [
+        "conv2d_relu y=nhwc", "conv2d_relu+maxpool2d(2,2) x=nhwc", "reshape", "dense_relu",
+        "dense+softmax"]
+
+
+def test_mlp_chain_plan():
+    # README.md:40-46: dense<w1, b1>..relu.., dense<w3, b3>..softmax
+    c = T.Chain(("dense", z(784, 1024), z(1024)), "relu", ("dense", z(1024, 1024), z(1024)),
+                "relu", ("dense", z(1024, 10), z(10)), "softmax")
+    assert c.plan((1024, 784)) == ["dense_relu", "dense_relu", "dense+softmax"]
+    c = T.Chain(("dense_relu", z(8, 4)), "softmax")
+    assert c.plan((2, 8)) == ["dense_relu+softmax"]
+
+
+W = "w"  # a weight tensor of the given shape, made inside the test
+
+
+@pytest.mark.parametrize("layers,shape,plan", [
+    # consumer with C % 16 != 0 takes the NCHW gather path: no NHWC intermediate
+    ([("conv2d", (W, 12, 3, 3, 3)), ("conv2d", (W, 8, 12, 3, 3))], (2, 3, 9, 9),
+     ["conv2d", "conv2d"]),
+    # consumer 1x1 over 16 channels is a direct conv (K = 16 <= 32): NCHW
+    ([("conv2d", (W, 16, 1, 3, 3)), ("conv2d", (W, 8, 16, 1, 1))], (2, 1, 9, 9),
+     ["conv2d", "conv2d"]),
+    # a relu between two convs joins the first; three convs chain NHWC twice
+    ([("conv2d", (W, 32, 1, 3, 3)), "relu", ("conv2d", (W, 32, 32, 3, 3)),
+      ("conv2d", (W, 16, 32, 3, 3))],
+     (2, 1, 12, 12), ["conv2d_relu y=nhwc", "conv2d x=nhwc y=nhwc", "conv2d x=nhwc"]),
+    # a pool that is not 2x2 stride 2 stays its own kernel
+    ([("conv2d_relu", (W, 16, 16, 3, 3)), ("maxpool2d", 3, 2)], (1, 16, 9, 9),
+     ["conv2d_relu", "maxpool2d(3,2)"]),
+    ([("conv2d_relu", (W, 16, 16, 3, 3)), ("maxpool2d", 2)], (1, 16, 9, 9),
+     ["conv2d_relu+maxpool2d(2,2)"]),
+    # a pooled conv writes NCHW (the pool output is the chain's tensor)
+    ([("conv2d", (W, 32, 1, 3, 3)), ("maxpool2d", 2, 2), ("conv2d", (W, 8, 32, 3, 3))],
+     (2, 1, 14, 14), ["conv2d+maxpool2d(2,2)", "conv2d"]),
+    # standalone relu / softmax / pool / reshape
+    (["relu", "softmax"], (3, 4), ["relu", "softmax"]),
+    ([("maxpool2d", 2, 2), ("reshape", 2, 8)], (2, 2, 4, 4), ["maxpool2d(2,2)", "reshape"]),
+])
+def test_chain_plans(layers, shape, plan):
+    def build(layer):
+        if isinstance(layer, str):
+            return layer
+        return (layer[0],) + tuple(z(*a[1:]) if isinstance(a, tuple) and a[0] == W else a
+                                   for a in layer[1:])
+    c = T.Chain(*[build(layer) for layer in layers])
+    assert c.plan(shape) == plan
+
+
+def test_chain_append_errors_use_layer_texts():
+    with pytest.raises(T.CamelError, match="Unrecognized layer operator: tensor:matmul"):
+        T.Chain(("tensor:matmul",))
+    with pytest.raises(T.CamelError, match="dense requires weights"):
+        T.Chain(("dense",))
+    with pytest.raises(T.CamelError, match="conv2d requires weights"):
+        T.Chain(("conv2d_relu",))
+    with pytest.raises(T.CamelError, match="conv2d requires rank-4"):
+        T.Chain(("conv2d", z(3, 3)))
+    with pytest.raises(T.CamelError, match="Expected integer argument"):
+        T.Chain(("maxpool2d", 2.5))
+
+
+def test_chain_handles():
+    c = T.Chain("relu")
+    c.release()
+    lib = T.load()
+    assert lib.camel_chain_release(c.handle or 12345) == T.ERR_ARG
+    out = T.C.c_uint64()
+    assert lib.camel_chain_apply(777, 0, T.C.byref(out)) == T.ERR_ARG

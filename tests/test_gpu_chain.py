@@ -1,0 +1,129 @@
+"""Composed layer chains on the GPU: x -> chain equals the layer-by-layer
+operator calls (tensor:dense_relu, tensor:conv2d_relu, tensor:maxpool2d, ...)
+that the chain stands for.  The fused groups compute the same values, so
+the comparison is bit for bit (the pooled convolution included: at these
+sizes it runs as one launch of one tile shape, so every output sums in the
+same order).  The layer-by-layer results are pinned against the oracle by
+tests/test_gpu_operators.py and tests/test_gpu_fusion.py."""
+import numpy as np
+import pytest
+
+from camel_amd import datagen as D
+from camel_amd import tensor as T
+from oracle import ffi as O
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+
+
+@pytest.fixture(autouse=True)
+def _release():
+    yield
+    T.release_all()
+
+
+def t(a):
+    return T.Tensor.from_numpy(np.asarray(a))
+
+
+def test_mlp_chain_equals_layer_calls():
+    # README.md:40-46 / BASELINE config 2 at batch 256
+    dims = [784, 1024, 1024, 10]
+    x = D.uniform(0x6000, (256, 784), 0.0, 1.0)
+    ws = [t(D.normal(0x6001 + i, (dims[i], dims[i + 1]), std=float(np.sqrt(1.0 / dims[i]))))
+          for i in range(3)]
+    bs = [t(D.uniform(0x6005 + i, (dims[i + 1],), -0.1, 0.1)) for i in range(3)]
+    chain = T.Chain(("dense", ws[0], bs[0]), "relu", ("dense", ws[1], bs[1]), "relu",
+                    ("dense", ws[2], bs[2]), "softmax")
+    assert chain.plan((256, 784)) == ["dense_relu", "dense_relu", "dense+softmax"]
+    xt = t(x)
+    got = chain(xt)
+    h = T.call("dense_relu", xt, with_=(ws[0], bs[0]))
+    h = T.call("dense_relu", h, with_=(ws[1], bs[1]))
+    h = T.call("dense", h, with_=(ws[2], bs[2]))
+    ref = T.call("softmax", h)
+    assert got.shape == (256, 10)
+    # the chain's output is a device tensor like any operator result
+    assert got.residency() == (False, True)
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+    p = O.softmax_rows(h.numpy())
+    assert np.max(np.abs(got.numpy() - p) / np.maximum(p, 1e-30)) <= 1e-6
+    chain.release()
+
+
+def test_cnn_chain_equals_layer_calls():
+    # BASELINE config 5 at batch 16: NHWC intermediate, fused pool, fused softmax
+    B = 16
+    x = D.uniform(0x6100, (B, 1, 28, 28), 0.0, 1.0)
+    w1 = t(D.normal(0x6101, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9))))
+    w2 = t(D.normal(0x6102, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288))))
+    w3 = t(D.normal(0x6103, (9216, 128), std=float(np.sqrt(2.0 / 9216))))
+    w4 = t(D.normal(0x6104, (128, 10), std=float(np.sqrt(2.0 / 128))))
+    b1, b2 = t(D.uniform(0x6105, (32,), -0.1, 0.1)), t(D.uniform(0x6106, (64,), -0.1, 0.1))
+    b3, b4 = t(D.uniform(0x6107, (128,), -0.1, 0.1)), t(D.uniform(0x6108, (10,), -0.1, 0.1))
+    chain = T.Chain(("conv2d_relu", w1, b1), ("conv2d_relu", w2, b2), ("maxpool2d", 2, 2),
+                    ("reshape", B, 9216), ("dense_relu", w3, b3), ("dense", w4, b4), "softmax")
+    assert chain.plan((B, 1, 28, 28)) == [
+        "conv2d_relu y=nhwc", "conv2d_relu+maxpool2d(2,2) x=nhwc", "reshape", "dense_relu",
+        "dense+softmax"]
+    xt = t(x)
+    got = chain(xt)
+    h = T.call("conv2d_relu", xt, with_=(w1, b1))
+    h = T.call("conv2d_relu", h, with_=(w2, b2))
+    h = T.call("maxpool2d", h, with_=(2, 2))
+    h = T.call("reshape", h, [B, 9216])
+    h = T.call("dense_relu", h, with_=(w3, b3))
+    h = T.call("dense", h, with_=(w4, b4))
+    ref = T.call("softmax", h)
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+    chain.release()
+
+
+def test_conv_chain_with_padding_stride_and_three_convs():
+    # conv -> conv -> conv through two NHWC intermediates, then a 3x3 pool
+    x = D.normal(0x6200, (3, 3, 20, 18))
+    ws = [t(D.normal(0x6201, (32, 3, 3, 3)) * F(0.2)), t(D.normal(0x6202, (48, 32, 3, 3)) * F(0.06)),
+          t(D.normal(0x6203, (16, 48, 1, 1)) * F(0.15))]
+    bs = [t(D.uniform(0x6204 + i, (n,), -0.1, 0.1)) for i, n in enumerate((32, 48, 16))]
+    chain = T.Chain(("conv2d_relu", ws[0], bs[0], 1, 1), ("conv2d", ws[1], bs[1], 2, 1), "relu",
+                    ("conv2d_relu", ws[2], bs[2]), ("maxpool2d", 3, 2))
+    assert chain.plan((3, 3, 20, 18)) == [
+        "conv2d_relu y=nhwc", "conv2d_relu x=nhwc y=nhwc", "conv2d_relu x=nhwc", "maxpool2d(3,2)"]
+    xt = t(x)
+    got = chain(xt)
+    h = T.call("conv2d_relu", xt, with_=(ws[0], bs[0], 1, 1))
+    h = T.call("conv2d", h, with_=(ws[1], bs[1], 2, 1))
+    h = T.call("relu", h)
+    h = T.call("conv2d_relu", h, with_=(ws[2], bs[2]))
+    ref = T.call("maxpool2d", h, with_=(3, 2))
+    assert got.shape == ref.shape
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+    chain.release()
+
+
+def test_chain_errors_match_the_failing_layer():
+    x = t(D.uniform(0x6300, (4, 8), -1.0, 1.0))
+    chain = T.Chain(("dense", t(np.zeros((9, 3), F))), "softmax")
+    with pytest.raises(T.CamelError, match="dense dimension mismatch"):
+        chain(x)
+    conv = T.Chain(("conv2d", t(np.zeros((4, 2, 3, 3), F))), ("maxpool2d", 2, 2))
+    with pytest.raises(T.CamelError, match="conv2d channel mismatch"):
+        conv(t(np.zeros((1, 3, 8, 8), F)))
+    with pytest.raises(T.CamelError, match="maxpool2d window larger than input"):
+        conv(t(np.zeros((1, 2, 4, 3), F)))
+    w = t(np.zeros((8, 3), F))
+    dangling = T.Chain(("dense", w))
+    w.release()
+    with pytest.raises(T.CamelError, match="chain layer weights were released"):
+        dangling(x)
+    for c in (chain, conv, dangling):
+        c.release()
+
+
+def test_empty_and_single_layer_chains():
+    x = t(D.uniform(0x6400, (5, 7), -1.0, 1.0))
+    same = T.Chain()(x)
+    np.testing.assert_array_equal(same.numpy(), x.numpy())
+    r = T.Chain("relu")(x)
+    np.testing.assert_array_equal(r.numpy(), T.call("relu", x).numpy())
