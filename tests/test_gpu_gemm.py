@@ -180,3 +180,41 @@ def test_generic_matmul_int64_bool_is_exact():
     H.call("camel_hip_matmul_generic", H.DT_I64, P(da.ptr), H.DT_BOOL, P(db.ptr), H.DT_I64,
            P(dc.ptr), 6, 4, 5)
     assert np.array_equal(K.host(dc, np.int64, (6, 4)), ref)
+
+
+@pytest.mark.parametrize("M,N,Kd", [
+    (130, 96, 200),    # MFMA tiles with ragged edges
+    (300, 7, 64),      # thin-N kernel
+    (16, 512, 300),    # skinny streaming kernel
+    (1024, 1024, 64),  # guard-free interior tiles
+])
+def test_sgemm_special_values_propagate_like_the_reference(M, N, Kd):
+    # inf / NaN in the operands: inf*0 = NaN, inf + (-inf) = NaN, NaN absorbs
+    # -- the same IEEE rules in the fp32 MFMA as in the reference's fp64 loop,
+    # so the non-finite outputs match exactly and the finite ones stay within
+    # the GEMM bar.  (Finite operands whose products or partial sums pass the
+    # fp32 range are the one known difference: the fp64 accumulator of the
+    # reference does not overflow there; see the design notes.)
+    rng = np.random.default_rng(M * 31 + N)
+    a, b = _ab(M, N, Kd, 0x4300 + M + N + Kd)
+    for arr in (a, b):
+        flat = arr.reshape(-1)
+        idx = rng.choice(flat.size, size=6, replace=False)
+        flat[idx[:2]] = np.inf
+        flat[idx[2:4]] = -np.inf
+        flat[idx[4:]] = np.nan
+    a[3, :] = 0.0
+    a[3, 5] = np.inf                      # row 3: inf * B[5, j] -> +-inf or NaN (B zero -> NaN)
+    b[5, :8] = 0.0
+    ref = O.matmul(a, b)
+    got = K.sgemm(a, b)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    # finite entries: the GEMM bar over the finite terms of each dot product
+    af = np.where(np.isfinite(a), a, 0).astype(np.float64)
+    bf = np.where(np.isfinite(b), b, 0).astype(np.float64)
+    bound = 1e-5 * np.sqrt(Kd) * (np.abs(af) @ np.abs(bf))
+    err = np.abs(got.astype(np.float64)[fin] - ref.astype(np.float64)[fin])
+    assert np.all(err <= bound[fin] + 1e-30)
