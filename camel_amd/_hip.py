@@ -23,7 +23,7 @@ DT_F32, DT_I64, DT_BOOL = 0, 1, 2
 OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_POW = range(5)
 CMP_LT, CMP_LE, CMP_GT, CMP_GE, CMP_EQ = range(5)
 EPI_NONE, EPI_BIAS, EPI_RELU = 0, 1, 2
-CONV_X_NHWC, CONV_Y_NHWC = 0x100, 0x200
+CONV_X_NHWC, CONV_Y_NHWC, CONV_W_PACKED = 0x100, 0x200, 0x400
 
 NP_DTYPE = {DT_F32: np.float32, DT_I64: np.int64, DT_BOOL: np.uint8}
 DT_OF_NP = {np.dtype(np.float32): DT_F32, np.dtype(np.int64): DT_I64,
@@ -63,6 +63,7 @@ _SIGNATURES = {
     "camel_hip_matmul_generic": [_I, _P, _I, _P, _I, _P, _I64, _I64, _I64],
     "camel_hip_conv2d": [_P, _P, _P, _P] + [_I64] * 9 + [_I],
     "camel_hip_conv2d_pool2": [_P, _P, _P, _P] + [_I64] * 9 + [_I],
+    "camel_hip_conv2d_pack_weights": [_P, _P] + [_I64] * 4,
     "camel_hip_dense_softmax": [_P, _P, _P, _P, _I64, _I64, _I64, _I],
     "camel_hip_maxpool2d": [_P, _P] + [_I64] * 7,
     "camel_hip_binary": [_I, _I, _P, _I, _P, _I, _P, _I64],

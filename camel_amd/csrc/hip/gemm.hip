@@ -1613,6 +1613,17 @@ int transpose_images(const float *src, float *dst, int64_t N, int64_t A, int64_t
     return check_launch("nchw_to_nhwc_kernel");
 }
 
+// w [Co][C][KHW] -> wp [Co][KHW][C] (the K order (kh, kw, c) of the NHWC
+// implicit GEMM): the transpose kernel's weight slice, launched alone (a
+// grid of one z slice is all weight slice).  With C and KHW exchanged the
+// same launch unpacks.
+int pack_weights(const float *w, float *wp, int64_t Co, int64_t C, int64_t KHW) {
+    hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, dim3(grid_for(Co * C * KHW, 256), 1, 1),
+                       dim3(256), 0, stream(), nullptr, nullptr, (int)C, 0, w, wp, (int)Co,
+                       (int)KHW);
+    return check_launch("nchw_to_nhwc_kernel");
+}
+
 // Pooled scratch owned for the duration of one entry point call (returned
 // to the stream-ordered pool on scope exit).
 struct Scratch {
@@ -1656,10 +1667,15 @@ GemmArgs conv_args(const float *w, const float *x, const float *bias, float *y, 
 template <class T>
 int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
                 int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
-                int64_t pad, int64_t OH, int64_t OW, int flags, bool x_nhwc, bool pool) {
+                int64_t pad, int64_t OH, int64_t OW, int flags, bool x_nhwc, bool pool,
+                bool w_packed) {
     const int64_t HW = H * W, K = C * KH * KW;
     Scratch xt, wt;
-    CAMEL_RETURN_IF(wt.alloc((size_t)(Co * K) * sizeof(float)));
+    // packed weights (already (kh, kw, c)): nothing to reorder; the
+    // transpose's weight slice is then given none
+    const int64_t co_reorder = w_packed ? 0 : Co;
+    if (!w_packed) CAMEL_RETURN_IF(wt.alloc((size_t)(Co * K) * sizeof(float)));
+    const float *wk = w_packed ? w : wt.f();
     if (!x_nhwc) {
         CAMEL_RETURN_IF(xt.alloc((size_t)(N * C * HW) * sizeof(float)));
         // xt comes from the pool (256-byte aligned); x is 16-byte aligned here.
@@ -1668,18 +1684,15 @@ int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int
         dim3 tgrid((unsigned)((HW + tp - 1) / tp), (unsigned)((C + 31) / 32), (unsigned)(N + 1));
         if (vec)
             hipLaunchKernelGGL(nchw_to_nhwc_kernel<true>, tgrid, dim3(256), 0, stream(), x, xt.f(),
-                               (int)C, (int)HW, w, wt.f(), (int)Co, (int)(KH * KW));
+                               (int)C, (int)HW, w, wt.f(), (int)co_reorder, (int)(KH * KW));
         else
             hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, tgrid, dim3(256), 0, stream(), x, xt.f(),
-                               (int)C, (int)HW, w, wt.f(), (int)Co, (int)(KH * KW));
-    } else {
-        // weights only: a grid of one z slice is all weight slice
-        hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, dim3(grid_for(Co * K, 256), 1, 1), dim3(256),
-                           0, stream(), nullptr, nullptr, (int)C, (int)HW, w, wt.f(), (int)Co,
-                           (int)(KH * KW));
+                               (int)C, (int)HW, w, wt.f(), (int)co_reorder, (int)(KH * KW));
+        CAMEL_RETURN_IF(check_launch("nchw_to_nhwc_kernel"));
+    } else if (!w_packed) {
+        CAMEL_RETURN_IF(pack_weights(w, wt.f(), Co, C, KH * KW));
     }
-    CAMEL_RETURN_IF(check_launch("nchw_to_nhwc_kernel"));
-    GemmArgs g = conv_args(wt.f(), x_nhwc ? x : xt.f(), bias, y, N, C, H, W, Co, KH, KW, stride, pad,
+    GemmArgs g = conv_args(wk, x_nhwc ? x : xt.f(), bias, y, N, C, H, W, Co, KH, KW, stride, pad,
                            OH, OW, flags);
     if (pool) {
         g.PW = (int)(OW / 2);
@@ -1756,7 +1769,8 @@ int conv_check(const float *x, const float *w, const float *bias, const float *y
     const int64_t K = C * KH * KW, P = OH * OW, NP = N * P;
     if (N * C * H * W > INT32_MAX || NP > INT32_MAX || N * Co * P > INT32_MAX || Co * K > INT32_MAX)
         return fail(CAMEL_HIP_ERR_SHAPE, name + ": tensor too large");
-    if (flags & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU | CAMEL_CONV_X_NHWC | CAMEL_CONV_Y_NHWC))
+    if (flags & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU | CAMEL_CONV_X_NHWC | CAMEL_CONV_Y_NHWC |
+                  CAMEL_CONV_W_PACKED))
         return fail(CAMEL_HIP_ERR_ARG, name + ": unknown flags");
     if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, name + ": null bias");
     if (N > 0 && (!x || !w || !y)) return fail(CAMEL_HIP_ERR_ARG, name + ": null operand");
@@ -1780,17 +1794,27 @@ int conv2d_run(const float *x, const float *w, const float *bias, float *y, int6
     // (the NCHW -> NHWC transpose runs one image per grid z, plus one z for
     // the weights)
     const bool gemm_nhwc = K > DIRECT_MAX_K && aligned && C % 16 == 0 && N < 65535;
+    bool w_packed = (flags & CAMEL_CONV_W_PACKED) != 0;
+    Scratch wu;
+    if (w_packed && !gemm_nhwc) {
+        // the other kernels read w [Co][C][KH][KW]: unpack into scratch
+        CAMEL_RETURN_IF(wu.alloc((size_t)(Co * K) * sizeof(float)));
+        CAMEL_RETURN_IF(pack_weights(w, wu.f(), Co, KH * KW, C));
+        w = wu.f();
+        w_packed = false;
+        flags &= ~CAMEL_CONV_W_PACKED;
+    }
     auto nhwc_gemm = [&](float *out, bool pooled) -> int {
         const bool k32 = C % 32 == 0;
         if (Co > 64)
             return k32 ? conv2d_nhwc<TileConv>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH,
-                                              OW, epi, x_nhwc, pooled)
+                                              OW, epi, x_nhwc, pooled, w_packed)
                        : conv2d_nhwc<TileConv16>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad,
-                                                OH, OW, epi, x_nhwc, pooled);
+                                                OH, OW, epi, x_nhwc, pooled, w_packed);
         return k32 ? conv2d_nhwc<TileConv64>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH,
-                                            OW, epi, x_nhwc, pooled)
+                                            OW, epi, x_nhwc, pooled, w_packed)
                    : conv2d_nhwc<TileConv64k16>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad,
-                                               OH, OW, epi, x_nhwc, pooled);
+                                               OH, OW, epi, x_nhwc, pooled, w_packed);
     };
     if (pool) {
         if (gemm_nhwc) return nhwc_gemm(y, true);
@@ -1935,6 +1959,18 @@ int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
     CAMEL_RETURN_IF(conv2d_run(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, flags, false));
+    return ok();
+}
+
+int camel_hip_conv2d_pack_weights(const float *w, float *wp, int64_t Co, int64_t C, int64_t KH,
+                                  int64_t KW) {
+    if (Co < 0 || C < 0 || KH < 0 || KW < 0) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d_pack_weights: negative dimension");
+    if (Co * C * KH * KW > INT32_MAX) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d_pack_weights: tensor too large");
+    if (Co * C * KH * KW == 0) return ok();
+    if (!w || !wp) return fail(CAMEL_HIP_ERR_ARG, "conv2d_pack_weights: null pointer");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(pack_weights(w, wp, Co, C, KH * KW));
     return ok();
 }
 

@@ -71,9 +71,9 @@ struct Activation {
     }
 };
 
-const TensorObject *requireLive(const TensorObject *t) {
-    if (t && !isLiveTensor(t)) throw std::invalid_argument("chain layer weights were released");
-    return t;
+void requireLive(const TensorObject *t, const std::shared_ptr<Storage> &storage) {
+    if (t && (!isLiveTensor(t) || t->storage() != storage))
+        throw std::invalid_argument("chain layer weights were released");
 }
 
 } // namespace
@@ -106,8 +106,35 @@ void LayerChain::append(const std::string &name, std::vector<const TensorObject 
     }
     s.w = tensor(0);
     s.bias = tensor(1);
+    if (s.w) s.w_storage = s.w->storage();
+    if (s.bias) s.bias_storage = s.bias->storage();
     s.ints = std::move(ints);
     steps_.push_back(std::move(s));
+    std::lock_guard<std::mutex> lock(pack_mutex_);
+    packed_.push_back(nullptr);
+}
+
+LayerChain::~LayerChain() {
+    for (void *p : packed_)
+        if (p) camel_hip_free(p);
+}
+
+const void *LayerChain::packedWeights(size_t i) const {
+    std::lock_guard<std::mutex> lock(pack_mutex_);
+    if (!packed_[i]) {
+        const TensorObject *w = steps_[i].w;
+        void *p = nullptr;
+        checkHip(camel_hip_malloc(&p, w->byteSize()));
+        const int rc = camel_hip_conv2d_pack_weights(static_cast<const float *>(w->deviceData()),
+                                                     static_cast<float *>(p), w->dim(0), w->dim(1),
+                                                     w->dim(2), w->dim(3));
+        if (rc != CAMEL_HIP_OK) {
+            camel_hip_free(p);
+            checkHip(rc);
+        }
+        packed_[i] = p;
+    }
+    return packed_[i];
 }
 
 std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> shape) const {
@@ -149,6 +176,7 @@ std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> sha
                 ++j;
             }
             g.x_nhwc = !groups.empty() && groups.back().kind == Group::Conv && groups.back().y_nhwc;
+            g.w_packed = batch >= 0 && readsNhwc(s, batch);
             g.y_nhwc = !g.pool && j < n && steps_[j].kind == LayerKind::Conv2d && batch >= 0 &&
                        readsNhwc(steps_[j], batch);
             break;
@@ -212,8 +240,8 @@ std::string LayerChain::plan(std::span<const int64_t> shape) const {
 
 TensorObject *LayerChain::apply(const TensorObject *x) const {
     for (const LayerStep &s : steps_) {
-        requireLive(s.w);
-        requireLive(s.bias);
+        requireLive(s.w, s.w_storage);
+        requireLive(s.bias, s.bias_storage);
     }
     Activation cur;
     cur.tensor = x;
@@ -265,7 +293,8 @@ TensorObject *LayerChain::apply(const TensorObject *x) const {
             if (numel > 0) {
                 const void *xin = cur.nhwc ? cur.nhwc : cur.tensor->deviceData();
                 const int layout = (g.x_nhwc ? CAMEL_CONV_X_NHWC : 0) | (g.y_nhwc ? CAMEL_CONV_Y_NHWC : 0);
-                conv2dLaunch(xin, cur.shape, s.w, s.bias, stride, pad, g.relu, g.pool, layout, y);
+                const void *wp = g.w_packed ? packedWeights((size_t)(&s - steps_.data())) : nullptr;
+                conv2dLaunch(xin, cur.shape, s.w, s.bias, stride, pad, g.relu, g.pool, layout, y, wp);
             }
             break;
         }

@@ -11,6 +11,8 @@
 //   conv2d (+relu) + maxpool2d(2, 2)  -> camel_hip_conv2d_pool2
 //   conv2d -> conv2d that reads NHWC  -> the first writes NHWC and the second
 //                                        reads it in place (no transpose)
+// A conv2d that runs as the NHWC implicit GEMM gets its weights packed once
+// per chain (camel_hip_conv2d_pack_weights) instead of once per call.
 // Every group's values equal the layer-by-layer operators' bit for bit,
 // except conv2d + maxpool2d where the partial last round of a large
 // convolution may sum a pixel in another tile shape (within the conv2d
@@ -19,6 +21,8 @@
 
 #include "tensor_object.h"
 
+#include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -33,10 +37,18 @@ struct LayerStep {
     const TensorObject *bias = nullptr; // optional bias
     std::vector<int64_t> ints;          // conv2d: stride, pad; maxpool2d: kernel, stride;
                                         // reshape: the target shape
+    // payload blocks of w and bias when appended: a handle released and
+    // reused for another tensor is caught at apply
+    std::shared_ptr<Storage> w_storage, bias_storage;
 };
 
 class LayerChain {
 public:
+    LayerChain() = default;
+    LayerChain(const LayerChain &) = delete;
+    LayerChain &operator=(const LayerChain &) = delete;
+    ~LayerChain();
+
     // Appends the layer operator `name` ("dense", "dense_relu", "relu",
     // "softmax", "conv2d", "conv2d_relu", "maxpool2d", "reshape"; a
     // "tensor:" prefix is accepted) with its bind arguments: leading tensors
@@ -59,9 +71,15 @@ private:
         bool pool = false;     // conv + maxpool2d(2, 2)
         bool x_nhwc = false;   // conv input comes NHWC from the previous conv
         bool y_nhwc = false;   // conv output goes NHWC to the next conv
+        bool w_packed = false; // conv runs as the NHWC GEMM: weights packed once
     };
     std::vector<Group> schedule(std::span<const int64_t> shape) const;
+    // The packed form of step i's conv weights (made on first use; tensors
+    // never change once made, so it stays valid while the chain lives).
+    const void *packedWeights(size_t i) const;
     std::vector<LayerStep> steps_;
+    mutable std::mutex pack_mutex_;
+    mutable std::vector<void *> packed_;
 };
 
 } // namespace camel_amd::tensor

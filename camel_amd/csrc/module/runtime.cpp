@@ -506,13 +506,15 @@ std::array<int64_t, 4> conv2dOutputShape(std::span<const int64_t> xs, TypeCode x
 
 void conv2dLaunch(const void *x, std::span<const int64_t> xs, const TensorObject *w,
                   const TensorObject *bias, int64_t stride, int64_t pad, bool relu, bool pool,
-                  int layout, void *y) {
+                  int layout, void *y, const void *w_packed) {
     const int64_t C = xs[1], KH = w->dim(2), KW = w->dim(3);
     if (C == 0 || KH == 0 || KW == 0) throw std::invalid_argument("conv2d requires a non-empty kernel");
-    const int flags = (bias ? CAMEL_EPI_BIAS : 0) | (relu ? CAMEL_EPI_RELU : 0) | layout;
+    const int flags = (bias ? CAMEL_EPI_BIAS : 0) | (relu ? CAMEL_EPI_RELU : 0) | layout |
+                      (w_packed ? CAMEL_CONV_W_PACKED : 0);
     const float *b = bias ? static_cast<const float *>(bias->deviceData()) : nullptr;
+    const void *wd = w_packed ? w_packed : w->deviceData();
     auto *fn = pool ? camel_hip_conv2d_pool2 : camel_hip_conv2d;
-    checkHip(fn(static_cast<const float *>(x), static_cast<const float *>(w->deviceData()), b,
+    checkHip(fn(static_cast<const float *>(x), static_cast<const float *>(wd), b,
                 static_cast<float *>(y), xs[0], C, xs[2], xs[3], w->dim(0), KH, KW, stride, pad,
                 flags));
 }

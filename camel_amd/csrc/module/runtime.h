@@ -71,9 +71,10 @@ std::array<int64_t, 4> conv2dOutputShape(std::span<const int64_t> xs, TypeCode x
                                          int64_t stride, int64_t pad);
 // Runs a checked conv2d on device memory: x and y are NCHW unless `layout`
 // carries CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC; pool adds maxpool2d(2, 2)
-// (y is then the pooled NCHW result).
+// (y is then the pooled NCHW result); w_packed, if given, is w already
+// packed by camel_hip_conv2d_pack_weights.
 void conv2dLaunch(const void *x, std::span<const int64_t> xs, const TensorObject *w,
                   const TensorObject *bias, int64_t stride, int64_t pad, bool relu, bool pool,
-                  int layout, void *y);
+                  int layout, void *y, const void *w_packed = nullptr);
 
 } // namespace camel_amd::tensor

@@ -56,8 +56,13 @@ enum camel_hip_compare_op {
 enum camel_hip_epilogue { CAMEL_EPI_NONE = 0, CAMEL_EPI_BIAS = 1, CAMEL_EPI_RELU = 2 };
 /* Layout bits of the conv2d flags, for a fused layer chain that keeps an
  * intermediate in the layout its consumer reads: x given as [N, H, W, C],
- * y written as [N, OH, OW, Co].  Either is only an addressing change. */
-enum camel_hip_conv_layout { CAMEL_CONV_X_NHWC = 0x100, CAMEL_CONV_Y_NHWC = 0x200 };
+ * y written as [N, OH, OW, Co], w given as [Co, KH, KW, C] (packed once by
+ * camel_hip_conv2d_pack_weights).  Each is only an addressing change. */
+enum camel_hip_conv_layout {
+    CAMEL_CONV_X_NHWC = 0x100,
+    CAMEL_CONV_Y_NHWC = 0x200,
+    CAMEL_CONV_W_PACKED = 0x400
+};
 
 /* ---- runtime ------------------------------------------------------------- */
 /* Selects the device and creates the stream and device-side error flag.
@@ -125,17 +130,23 @@ int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int
 /* ---- conv2d / pooling (no reference op; defined by composition) --------- */
 /* y[N,Co,OH,OW] = conv(x[N,C,H,W], w[Co,C,KH,KW]) (+bias[Co]) (relu), NCHW,
  * implicit GEMM on the same MFMA core.  OH = (H+2*pad-KH)/stride+1.
- * flags may add CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC (same values, other
- * addressing). */
+ * flags may add CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC / CAMEL_CONV_W_PACKED
+ * (same values, other addressing). */
 int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y, int64_t N,
                      int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
                      int64_t stride, int64_t pad, int flags);
+/* wp[Co,KH,KW,C] = w[Co,C,KH,KW] reordered: the weight layout the NHWC
+ * implicit GEMM reads.  A caller that applies the same weights many times
+ * packs them once and passes CAMEL_CONV_W_PACKED (no reference counterpart:
+ * weight pre-packing of a layer chain). */
+int camel_hip_conv2d_pack_weights(const float *w, float *wp, int64_t Co, int64_t C, int64_t KH,
+                                  int64_t KW);
 /* y[N,Co,OH/2,OW/2] = maxpool2x2(conv2d(x) (+bias) (relu)), the
  * conv2d_relu..maxpool2d of a CNN fused: the 2x2 stride-2 max (the rule of
  * camel_hip_maxpool2d) is taken in the convolution's epilogue, so the
  * full-size result never reaches HBM.  No reference operator (compose is a
  * stub, src/builtin/operators/macro.cpp:30).  flags may add
- * CAMEL_CONV_X_NHWC; OH, OW >= 2. */
+ * CAMEL_CONV_X_NHWC / CAMEL_CONV_W_PACKED; OH, OW >= 2. */
 int camel_hip_conv2d_pool2(const float *x, const float *w, const float *bias, float *y, int64_t N,
                            int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
                            int64_t stride, int64_t pad, int flags);

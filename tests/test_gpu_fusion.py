@@ -263,3 +263,30 @@ def test_conv2d_pool2_large_schedules_match_conv_then_pool():
         diff = np.abs(got[:1].astype(np.float64) - ref[:1])
         assert np.all(diff <= 2e-5 * np.sqrt(Cin * kh * kw) * mag + 1e-30)
         assert np.all(np.abs(got.astype(np.float64) - ref) <= 1e-3)
+
+
+@pytest.mark.parametrize("geom", GEOMS + [(2, 64, 9, 9, 96, 3, 3, 2, 1)])
+def test_conv2d_packed_weights_change_addressing_only(geom):
+    # camel_hip_conv2d_pack_weights gives w as [Co, KH, KW, C]; a conv given
+    # CAMEL_CONV_W_PACKED reads it directly on the NHWC GEMM path and unpacks
+    # it on the others: the same values either way.
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    x = D.normal(0x5A00 + Cin, (N, Cin, H_, W_))
+    w = D.normal(0x5A01 + Co, (Co, Cin, kh, kw)) * F(np.sqrt(2.0 / (kh * kw * Cin)))
+    b = D.uniform(0x5A02, (Co,), -0.1, 0.1)
+    dw, dwp = K.dev(w), K.empty(w.nbytes)
+    H.call("camel_hip_conv2d_pack_weights", P(dw.ptr), P(dwp.ptr), Co, Cin, kh, kw)
+    assert np.array_equal(K.host(dwp, F, (Co, kh, kw, Cin)), w.transpose(0, 2, 3, 1))
+    epi = H.EPI_BIAS | H.EPI_RELU
+    dref, shape = _conv(x, w, b, geom, epi)
+    ref = K.host(dref, F, shape)
+    wp = K.host(dwp, F, (Co, kh, kw, Cin))
+    dy, _ = _conv(x, wp, b, geom, epi | H.CONV_W_PACKED)
+    np.testing.assert_array_equal(K.host(dy, F, shape), ref)
+    x_nhwc = np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+    dy, _ = _conv(x_nhwc, wp, b, geom, epi | H.CONV_W_PACKED | H.CONV_X_NHWC)
+    np.testing.assert_array_equal(K.host(dy, F, shape), ref)
+    if shape[2] >= 2 and shape[3] >= 2:
+        dpool, pshape = _conv(x, w, b, geom, epi, pooled=True)
+        dy, _ = _conv(x, wp, b, geom, epi | H.CONV_W_PACKED, pooled=True)
+        np.testing.assert_array_equal(K.host(dy, F, pshape), K.host(dpool, F, pshape))
