@@ -127,3 +127,34 @@ def test_empty_and_single_layer_chains():
     np.testing.assert_array_equal(same.numpy(), x.numpy())
     r = T.Chain("relu")(x)
     np.testing.assert_array_equal(r.numpy(), T.call("relu", x).numpy())
+
+
+def test_chain_int64_dense_and_softmax_follow_the_composition():
+    # non-Float32 operands: dense runs matmul + add through the device
+    # composition, then the softmax composition, as the layer calls do
+    x = t((np.arange(12).reshape(4, 3) - 5).astype(np.int64))
+    w = t((np.arange(6).reshape(3, 2) % 3).astype(np.int64))
+    chain = T.Chain(("dense", w), "softmax")
+    assert chain.plan((4, 3)) == ["dense+softmax"]
+    got = chain(x)
+    ref = T.call("softmax", T.call("dense", x, with_=(w,)))
+    assert got.dtype_code == ref.dtype_code
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+    chain.release()
+
+
+def test_conv_chain_without_nhwc_consumer_and_empty_batch():
+    # second conv has C % 16 != 0: NCHW between them; and a batch of 0
+    w1 = t(D.normal(0x6500, (12, 3, 3, 3)) * F(0.2))
+    w2 = t(D.normal(0x6501, (8, 12, 3, 3)) * F(0.1))
+    chain = T.Chain(("conv2d_relu", w1), ("conv2d", w2, None, 1, 1), ("maxpool2d", 2, 2))
+    assert chain.plan((2, 3, 10, 10)) == ["conv2d_relu", "conv2d+maxpool2d(2,2)"]
+    x = t(D.normal(0x6502, (2, 3, 10, 10)))
+    got = chain(x)
+    h = T.call("conv2d_relu", x, with_=(w1,))
+    h = T.call("conv2d", h, with_=(w2, None, 1, 1))
+    ref = T.call("maxpool2d", h, with_=(2, 2))
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+    empty = chain(t(np.zeros((0, 3, 10, 10), F)))
+    assert empty.shape == (0, 8, 4, 4)
+    chain.release()
