@@ -1,18 +1,19 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X tensor-module backend (one GPU).
 
-Headline (`value`): fp32 GEMM C = A.B at M=N=K=4096 (the
-size the north-star target is quoted on), GFLOP/s of the whole timed loop,
-inputs resident in HBM.  The `suite` object carries the other BASELINE
-configs measured the same way (MLP forward, GEMM sweep, conv2d, small CNN,
-elementwise and softmax bandwidth), each with its own roofline entry.
+Headline (`value`): fp32 GEMM C = A.B at M=N=K=4096, GFLOP/s of the whole
+timed loop, inputs resident in HBM.  The `suite` object carries the other
+benchmark workloads measured the same way (MLP forward, GEMM sweep, conv2d,
+small CNN, elementwise and softmax bandwidth), each with its own roofline
+entry.
 
 Timing: W warmup steps, device sync, then exactly K steps between two HIP
 events on the library stream (the stream every kernel is launched on),
 device sync after.  Suite entries warm up for at least 50 ms (the GPU clock
 ramps after idle time) and time at least 10 ms of work (microsecond kernels
-would otherwise measure host launch jitter); the CPU baseline runs last.  `roofline.achieved` = algorithmic FLOP (or bytes) of the
-dominant kernel per launch / its average launch time from those events.
+would otherwise measure host launch jitter); the CPU baseline runs last.
+`roofline.achieved` = algorithmic FLOP (or bytes) of the dominant kernel per
+launch / its average launch time from those events.
 
 The CPU baseline times the oracle (a loop-for-loop restatement of the
 reference's CPU kernels, single thread) on a bounded row slab of the same
@@ -169,7 +170,7 @@ def wl_skinny(steps, warmup):
 
 
 def wl_mlp(steps, warmup, fused=True):
-    """dense 784->1024->1024->10 (+relu) then row softmax, batch 1024.
+    """MLP forward: dense 784->1024->1024->10 (+relu) then row softmax, batch 1024.
     fused: the classifier layer and the softmax run as one kernel
     (camel_hip_dense_softmax); otherwise GEMM then the softmax kernel."""
     B = 1024
@@ -202,7 +203,7 @@ def wl_mlp(steps, warmup, fused=True):
 
 
 def wl_conv(steps, warmup):
-    """BASELINE config 4: conv2d 64x64x56x56 -> 128, 3x3, s1 p1, bias + relu."""
+    """conv2d 64x64x56x56 -> 128, 3x3, s1 p1, bias + relu."""
     x = D.normal(D.SEED_CONV_X, (64, 64, 56, 56))
     w = D.normal(D.SEED_CONV_W, (128, 64, 3, 3), std=float(np.sqrt(2.0 / (9 * 64))))
     b = np.zeros(128, np.float32)
@@ -216,7 +217,7 @@ def wl_conv(steps, warmup):
 
 
 def wl_cnn(steps, warmup, fused=True):
-    """small CNN forward, batch 512 (valid 3x3 convs, 2x2 pool).
+    """Small CNN forward, batch 512 (valid 3x3 convs, 2x2 pool).
     fused: conv1 writes NHWC for conv2 to read in place, conv2 + relu + pool
     are one kernel (camel_hip_conv2d_pool2, weights packed once at setup),
     and dense2 + softmax one more (camel_hip_dense_softmax); otherwise every

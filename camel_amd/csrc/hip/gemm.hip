@@ -1338,7 +1338,8 @@ __global__ __launch_bounds__(PIXB) void conv2d_direct_nhwc_kernel(
 // ---- host-side launch -----------------------------------------------------------
 
 // Tile shapes, chosen by measured sweeps on MI355X (GEMM 1024-8192, the
-// BASELINE conv shapes): 8 waves at 256x256 keep the accumulators in arch
+// benchmark conv shapes 64x64x56x56 -> 128 and 512x32x26x26 -> 64, 3x3): 8
+// waves at 256x256 keep the accumulators in arch
 // VGPRs without spills; the conv tiles are small enough for two work-groups
 // per CU, which hides the gather latency better than larger tiles do.
 using TileBig = Tile<256, 256, 32, 2, 4, 1, false>; // wave 128x64, 8 waves
@@ -1483,7 +1484,8 @@ using BandTile = Tile<64, (T::BK >= 32 ? 32 : 64), T::BK, 2, (T::BK >= 32 ? 1 : 
 //   * when every tile row sits in one tile-row group (tile id = tn * tiles_m
 //     + tm) the leftover tiles are whole tile columns, i.e. a column band,
 //     and that band runs as one launch of small tiles over all of K (no
-//     partials; measured faster than the split below at BASELINE config 4,
+//     partials; measured faster than the split below at the 64x64x56x56
+//     -> 128 3x3 conv,
 //     whose 1568 tiles leave 32 after 3 rounds);
 //   * otherwise the leftover tiles are split along K and reduced in order.
 template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, const char *name) {

@@ -28,7 +28,7 @@ def cnn_chain(c1=1, c2=32, c3=64):
 
 
 def test_cnn_chain_plan_fuses_every_pair():
-    # BASELINE config 5 as a chain: conv1 writes NHWC for conv2, conv2 + relu
+    # The benchmark small CNN as a chain: conv1 writes NHWC for conv2, conv2 + relu
     # + pool are one kernel, the classifier and the softmax one more.
     assert cnn_chain().plan((512, 1, 28, 28)) == [
         "conv2d_relu y=nhwc", "conv2d_relu+maxpool2d(2,2) x=nhwc", "reshape", "dense_relu",

@@ -28,7 +28,7 @@ def t(a):
 
 
 def test_mlp_chain_equals_layer_calls():
-    # README.md:40-46 / BASELINE config 2 at batch 256
+    # README.md:40-46: the benchmark MLP at batch 256
     dims = [784, 1024, 1024, 10]
     x = D.uniform(0x6000, (256, 784), 0.0, 1.0)
     ws = [t(D.normal(0x6001 + i, (dims[i], dims[i + 1]), std=float(np.sqrt(1.0 / dims[i]))))
@@ -53,7 +53,7 @@ def test_mlp_chain_equals_layer_calls():
 
 
 def test_cnn_chain_equals_layer_calls():
-    # BASELINE config 5 at batch 16: NHWC intermediate, fused pool, fused softmax
+    # The benchmark small CNN at batch 16: NHWC intermediate, fused pool, fused softmax
     B = 16
     x = D.uniform(0x6100, (B, 1, 28, 28), 0.0, 1.0)
     w1 = t(D.normal(0x6101, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9))))

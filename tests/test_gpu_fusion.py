@@ -56,8 +56,8 @@ def _dense_then_softmax(x, w, b, flags):
 
 
 @pytest.mark.parametrize("M,N,Kd,flags", [
-    (1024, 10, 1024, H.EPI_BIAS),               # BASELINE config 2 classifier
-    (512, 10, 128, H.EPI_BIAS),                 # BASELINE config 5 classifier
+    (1024, 10, 1024, H.EPI_BIAS),               # the benchmark MLP's classifier
+    (512, 10, 128, H.EPI_BIAS),                 # the benchmark CNN's classifier
     (300, 7, 50, H.EPI_BIAS | H.EPI_RELU),      # relu before the softmax
     (257, 32, 512, 0),                          # widest fused row, longest K for it
     (200, 3, 1, H.EPI_BIAS),                    # K = 1

@@ -4,7 +4,7 @@ oracle (a restatement of the reference kernels) on the same seeded inputs.
 
 They read like the reference's own NN programs: test/run/nn/tensor_smoke.cml
 (closed forms), mnist.cml (the composed softmax), svm.cml (the relu idiom)
-and the BASELINE MLP / CNN chains built from the layer operators.  They also
+and the benchmark MLP / CNN chains built from the layer operators.  They also
 check the residency contract: operator outputs stay on the device, and a
 chain of operators never copies through the host.
 """
@@ -54,7 +54,7 @@ def test_tensor_smoke_closed_forms():
 
 
 def test_matmul_config1_matches_oracle():
-    # 256^3, U(-1,1), seeds 0x5EED0001 / 0x5EED0002.
+    # The 256^3 plumbing case: U(-1,1), seeds 0x5EED0001 / 0x5EED0002.
     a = D.uniform(D.SEED_MATMUL_A, (256, 256), -1.0, 1.0)
     b = D.uniform(D.SEED_MATMUL_B, (256, 256), -1.0, 1.0)
     c = T.call("tensor:matmul", t(a), t(b))
@@ -127,7 +127,7 @@ def test_softmax_operator_matches_the_mnist_composition(rows, cols):
 
 
 def test_mlp_config2_chain_stays_on_device():
-    # dense<w,b>..relu chain 784 -> 1024 -> 1024 -> 10, softmax.
+    # The benchmark MLP: dense<w,b>..relu chain 784 -> 1024 -> 1024 -> 10, softmax.
     B, dims = 1024, [784, 1024, 1024, 10]
     x = D.uniform(D.SEED_MLP, (B, dims[0]), 0.0, 1.0)
     ws = [D.normal(D.SEED_MLP + 1 + i, (dims[i], dims[i + 1]), std=float(np.sqrt(1.0 / dims[i])))
@@ -169,7 +169,7 @@ def test_dense_bias_operand_forms_agree():
 
 
 def test_conv_pool_cnn_slice_matches_oracle():
-    # The small-CNN layers of BASELINE config 5 at batch 4.
+    # The benchmark small-CNN layers (28x28 -> 26 -> 24 -> pool 12) at batch 4.
     x = D.uniform(D.SEED_CNN, (4, 1, 28, 28), 0.0, 1.0)
     w1 = D.normal(D.SEED_CNN + 1, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
     w2 = D.normal(D.SEED_CNN + 2, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288)))
