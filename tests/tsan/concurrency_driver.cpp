@@ -2,9 +2,10 @@
 // layer's host-side paths at once, the way the reference's Taskflow scheduler
 // calls operators from worker threads (src/passes/sched/taskflow/taskflow.cpp:
 // 157-181, 474-513).  Every path here stays on the host (host-born tensors,
-// views, shape arrays, element reads, equality, printing, release), so it
-// runs without a GPU; what it exercises is the layer's shared state: the
-// object registry, the Storage residency state and the per-thread error text.
+// views, shape arrays, element reads, equality, printing, layer-chain
+// planning, release), so it runs without a GPU; what it exercises is the
+// layer's shared state: the object and chain registries, the Storage
+// residency state and the per-thread error text.
 //
 // Usage: concurrency_driver [threads] [iterations]; exit status 0 when every
 // result matched (ThreadSanitizer reports separately on stderr).
@@ -94,6 +95,30 @@ void worker(int id, int iterations) {
                 if (camel_tensor_release(view.slot)) fail(id, "release view");
             }
             camel_array_release(arr);
+        }
+        // A layer chain over host-born weights: created, extended, planned and
+        // released on every thread at once (the chain registry is shared).
+        {
+            const int64_t wshape[2] = {cols, 5};
+            std::vector<float> wdata((size_t)(cols * 5), 0.5f);
+            uint64_t w = 0, chain = 0;
+            if (camel_tensor_from_host(CAMEL_TC_FLOAT32, 2, wshape, wdata.data(), &w) ||
+                camel_chain_create(&chain)) {
+                fail(id, "chain setup");
+            } else {
+                camel_value wv{CAMEL_TC_TENSOR, w};
+                if (camel_chain_append(chain, "tensor:dense", 1, &wv) ||
+                    camel_chain_append(chain, "relu", 0, nullptr) ||
+                    camel_chain_append(chain, "softmax", 0, nullptr))
+                    fail(id, "chain append");
+                char plan[128];
+                size_t need = 0;
+                if (camel_chain_plan(chain, 2, shape, plan, sizeof plan, &need) ||
+                    std::strcmp(plan, "dense_relu+softmax\n") != 0)
+                    fail(id, "chain plan");
+                if (camel_chain_release(chain)) fail(id, "chain release");
+                if (camel_tensor_release(w)) fail(id, "release weights");
+            }
         }
         // An error on this thread must not leak into another thread's text.
         camel_value bad{CAMEL_TC_TENSOR, t}, out{};
