@@ -20,7 +20,8 @@
 //   * stages are double-buffered in LDS with the next stage held in registers
 //     while the current one is multiplied, one barrier per stage;
 //   * blockIdx is remapped so each of the 8 XCDs (own L2) works on a compact
-//     group of tiles, grouped GROUP_M tile-rows deep;
+//     group of tiles, grouped GROUP_M tile-rows deep (with K splits: on
+//     whole splits);
 //   * split-K (blockIdx.y) writes fp32 partials that tile_reduce_kernel sums in
 //     split order and passes through the epilogue;
 //   * epilogue: bias (per column for dense, per row = output channel for
@@ -132,15 +133,20 @@ __device__ __forceinline__ void tile_of(int id, int tiles_m, int tiles_n, int &t
     tn = in_group / gsize;
 }
 
-// Logical tile of this work-group.  A launch covers tiles [tile_begin,
-// tile_begin + gridDim.x); blockIdx.y is the K split.  Work-groups are
-// dispatched round-robin over the 8 XCDs, so a single-split launch gives XCD x
-// the contiguous id range [x*nb/8, (x+1)*nb/8) and its L2 a compact block.
-__device__ __forceinline__ int block_tile_id(int tile_begin) {
-    int bid = blockIdx.x;
-    const int nb = gridDim.x;
-    if (gridDim.y == 1 && (nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-    return tile_begin + bid;
+// Position of this work-group: its tile (local to the launch, which covers
+// tiles [tile_begin, tile_begin + gridDim.x)) and its K split (gridDim.y
+// splits).  Work-groups are dispatched round-robin over the 8 XCDs in linear
+// order (blockIdx.x fastest).  When the grid size nb is a multiple of 8, XCD x
+// is given the contiguous range [x*nb/8, (x+1)*nb/8) of (split, tile)
+// positions instead, so its L2 holds a compact block of tiles and, with K
+// splits, whole splits: the A and B panels of one K range are fetched from
+// HBM by one XCD rather than by every XCD that runs one of their tiles.
+__device__ __forceinline__ void block_pos(int &local, int &split) {
+    const int nt = gridDim.x, nb = nt * gridDim.y;
+    int bid = blockIdx.x + nt * blockIdx.y;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    split = bid / nt;
+    local = bid - split * nt;
 }
 
 template <class T, int AMODE, int BMODE>
@@ -150,10 +156,11 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     const int tid = threadIdx.x;
     const int tiles_m = (g.M + T::BM - 1) / T::BM;
     const int tiles_n = (g.N - g.n_begin + T::BN - 1) / T::BN;
-    int tm, tn;
-    tile_of(block_tile_id(g.tile_begin), tiles_m, tiles_n, tm, tn);
+    int local, split, tm, tn;
+    block_pos(local, split);
+    tile_of(g.tile_begin + local, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * T::BM, n0 = g.n_begin + tn * T::BN;
-    const int kbeg = blockIdx.y * g.k_per_split;
+    const int kbeg = split * g.k_per_split;
     const int kend = min(g.K, kbeg + g.k_per_split);
     const int nk = kend > kbeg ? (kend - kbeg + T::BK - 1) / T::BK : 0;
 
@@ -674,7 +681,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 if (row >= g.M) continue;
                 float x = acc[i][j][v];
                 if (g.partial) {
-                    g.partial[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * (T::BM * T::BN) +
+                    g.partial[((size_t)split * gridDim.x + local) * (T::BM * T::BN) +
                               (size_t)(row - m0) * T::BN + (col - n0)] = x;
                     continue;
                 }
