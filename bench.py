@@ -218,7 +218,7 @@ def wl_conv(steps, warmup):
 
 def wl_cnn(steps, warmup, fused=True):
     """Small CNN forward, batch 512 (valid 3x3 convs, 2x2 pool).
-    fused: conv1 writes NHWC for conv2 to read in place, conv2 + relu + pool
+    fused: conv1 writes NCHW4 for conv2 to read in place, conv2 + relu + pool
     are one kernel (camel_hip_conv2d_pool2, weights packed once at setup),
     and dense2 + softmax one more (camel_hip_dense_softmax); otherwise every
     layer is its own call."""
@@ -238,16 +238,16 @@ def wl_cnn(steps, warmup, fused=True):
     a5 = H.DeviceBuffer(B * 10 * 4)
     dp = H.DeviceBuffer(B * 10 * 4)
     EPI = H.EPI_BIAS | H.EPI_RELU
-    # conv2's weights packed once for the NHWC GEMM (weight pre-packing)
+    # conv2's weights packed once for the implicit GEMM (weight pre-packing)
     d2p = H.DeviceBuffer(64 * 32 * 9 * 4)
     H.call("camel_hip_conv2d_pack_weights", P(d2.ptr), P(d2p.ptr), 64, 32, 3, 3)
 
     def step():
         if fused:
             H.call("camel_hip_conv2d", P(dx.ptr), P(d1.ptr), P(b1.ptr), P(a1.ptr), B, 1, 28, 28, 32,
-                   3, 3, 1, 0, EPI | H.CONV_Y_NHWC)
+                   3, 3, 1, 0, EPI | H.CONV_Y_NCHW4)
             H.call("camel_hip_conv2d_pool2", P(a1.ptr), P(d2p.ptr), P(b2.ptr), P(a3.ptr), B, 32, 26,
-                   26, 64, 3, 3, 1, 0, EPI | H.CONV_X_NHWC | H.CONV_W_PACKED)
+                   26, 64, 3, 3, 1, 0, EPI | H.CONV_X_NCHW4 | H.CONV_W_PACKED)
             sgemm_call(a3, d3, a4, B, 128, 9216, b3, EPI)()
             H.call("camel_hip_dense_softmax", P(a4.ptr), P(d4.ptr), P(b4.ptr), P(dp.ptr), B, 10, 128,
                    H.EPI_BIAS)

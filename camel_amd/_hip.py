@@ -24,6 +24,7 @@ OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_POW = range(5)
 CMP_LT, CMP_LE, CMP_GT, CMP_GE, CMP_EQ = range(5)
 EPI_NONE, EPI_BIAS, EPI_RELU = 0, 1, 2
 CONV_X_NHWC, CONV_Y_NHWC, CONV_W_PACKED = 0x100, 0x200, 0x400
+CONV_X_NCHW4, CONV_Y_NCHW4 = 0x800, 0x1000
 
 NP_DTYPE = {DT_F32: np.float32, DT_I64: np.int64, DT_BOOL: np.uint8}
 DT_OF_NP = {np.dtype(np.float32): DT_F32, np.dtype(np.int64): DT_I64,

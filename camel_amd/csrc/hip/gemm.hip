@@ -98,9 +98,13 @@ struct GemmArgs {
     int tile_begin;   // first logical tile of the launch
     int n_begin;      // first column of the launch's tile grid (a column band)
     int flags;
-    // conv geometry (N = batch * P columns); Cin, KW only for LOAD_NHWC
+    // conv geometry (N = batch * P columns); Cin, KW, pxs, cqs only for
+    // LOAD_NHWC.  The channel-quad input layouts it reads put channels
+    // 4q .. 4q+3 of pixel (ih, iw) of image n at the 16 bytes starting at
+    // n * CHW + (ih * W + iw) * pxs + q * cqs floats: NHWC has pxs = Cin,
+    // cqs = 4; NCHW4 ([N][C/4][H][W][4]) has pxs = 4, cqs = 4 * H * W.
     int P, OW, H, W, CHW, stride, pad;
-    int Cin, KW;
+    int Cin, KW, pxs, cqs;
     // LOAD_NHWC_POOL: columns in pool order, 4 per window of a 2x2 stride-2
     // max pool over a PH x PW grid (PP = PH * PW windows per image); C is the
     // pooled output [batch][M][PP]
@@ -112,6 +116,13 @@ struct GemmArgs {
 template <int Q> __device__ __forceinline__ float quad_lane(float v) {
     constexpr int ctrl = Q | (Q << 2) | (Q << 4) | (Q << 6);
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xf, 0xf, false));
+}
+
+// Offset of conv output (image img, channel row, pixel p) in y: NCHW, or
+// NCHW4 ([N][M/4][P][4], M % 4 == 0) for q4.
+__device__ __forceinline__ size_t conv_out_off(const GemmArgs &g, bool q4, int img, int row, int p) {
+    return q4 ? (size_t)img * g.M * g.P + (size_t)(row & ~3) * g.P + 4 * (size_t)p + (row & 3)
+              : ((size_t)img * g.M + row) * g.P + p;
 }
 
 // LDS slot of B column n within a k-quad plane.  A 16-byte LDS access is
@@ -182,9 +193,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     };
     StageRegs R0;
 
-    // ---- NHWC conv: each thread's B items are fixed (pixel, k-quad) pairs.
-    // Pixel geometry is decoded once; the k-quad's (kh, kw, c) comes from the
-    // stage start (uniform: one stage never crosses a (kh, kw) boundary).
+    // ---- NHWC / NCHW4 conv: each thread's B items are fixed (pixel, k-quad)
+    // pairs.  Pixel geometry and the k-quad's channel-quad offset are decoded
+    // once; the stage's (kh, kw, c0) comes from the stage start (uniform: one
+    // stage never crosses a (kh, kw) boundary).
     int px_base[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
     int px_ih[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
     int px_iw[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
@@ -210,7 +222,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 }
                 px_ih[i] = oh * g.stride - g.pad;
                 px_iw[i] = ow * g.stride - g.pad;
-                px_base[i] = ((img * g.H + px_ih[i]) * g.W + px_iw[i]) * g.Cin;
+                px_base[i] = img * g.CHW + (px_ih[i] * g.W + px_iw[i]) * g.pxs + (q % T::KQ) * g.cqs;
             } else {
                 px_ih[i] = -(1 << 28); // never in range
                 px_iw[i] = 0;
@@ -272,15 +284,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             // k0 .. k0+BK-1 share (kh, kw): channels c0 .. c0+BK-1.
             const int khw = k0 / g.Cin, c0 = k0 - khw * g.Cin;
             const int kh = khw / g.KW, kw = khw - kh * g.KW;
-            const int koff = (kh * g.W + kw) * g.Cin + c0;
+            const int koff = (kh * g.W + kw) * g.pxs + (c0 >> 2) * g.cqs;
 #pragma unroll
             for (int i = 0; i < T::BN_ITEMS; ++i) {
-                const int q = tid + i * T::THREADS;
-                const int kq = q % T::KQ;
                 const int ih = px_ih[i] + kh, iw = px_iw[i] + kw;
                 rbn[i] = ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W &&
                           (FULL || k0 < kend))
-                             ? *reinterpret_cast<const float4 *>(g.B + (size_t)(px_base[i] + koff) + 4 * kq)
+                             ? *reinterpret_cast<const float4 *>(g.B + (size_t)(px_base[i] + koff))
                              : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
@@ -529,6 +539,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     // ---- epilogue ----
     const bool has_bias = (g.flags & CAMEL_EPI_BIAS) != 0 && g.partial == nullptr;
     const bool has_relu = (g.flags & CAMEL_EPI_RELU) != 0 && g.partial == nullptr;
+    // conv output in NCHW4 (the output rows of a lane's accumulator quad
+    // v = 4u .. 4u+3 are 4 consecutive channels starting at a multiple of 4:
+    // one 16-byte store per pixel)
+    const bool q4 = is_conv<BMODE> && (g.flags & CAMEL_CONV_Y_NCHW4) != 0;
     // Bias values come into registers before the stores that follow them: as
     // far as the compiler knows C may alias bias, so a bias load after a
     // store waits for that store, one L2 round trip per element (measured:
@@ -643,7 +657,23 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                     float *out;
                     if constexpr (is_conv<BMODE>) {
                         const int img = col / g.P, p = col - img * g.P;
-                        out = g.C + (size_t)img * g.M * g.P + p;
+                        out = g.C + (size_t)img * g.M * g.P + (q4 ? 4 * p : p);
+                        if (q4) {
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                const int row0 = m0 + wm * T::WTM + i * 32 + 8 * u + 4 * half;
+                                float4 o;
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    float x = acc[i][j][4 * u + r];
+                                    if constexpr (decltype(bias_tag)::value) x = x + brow[4 * u + r];
+                                    if constexpr (decltype(relu_tag)::value) x = relu_idiom(x);
+                                    o[r] = x;
+                                }
+                                *reinterpret_cast<float4 *>(out + (size_t)row0 * g.P) = o;
+                            }
+                            continue;
+                        }
                     } else {
                         out = g.C + col;
                     }
@@ -673,7 +703,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             size_t col_off = col;
             if constexpr (is_conv<BMODE>) {
                 const int img = col / g.P, p = col - img * g.P;
-                col_off = (size_t)img * g.M * g.P + p;
+                col_off = conv_out_off(g, q4, img, 0, p);
             }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
@@ -692,7 +722,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 }
                 if (has_relu) x = relu_idiom(x);
                 if constexpr (is_conv<BMODE>)
-                    g.C[col_off + (size_t)row * g.P] = x;
+                    g.C[col_off + (q4 ? (size_t)(row & ~3) * g.P + (row & 3) : (size_t)row * g.P)] = x;
                 else
                     g.C[(size_t)row * g.ldc + col] = x;
             }
@@ -702,7 +732,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 
 // Sums the K splits of tiles [tile_begin, tile_begin + ntiles) in split
 // order (so results do not depend on scheduling), then bias and relu, and
-// stores with the GEMM (row-major) or conv (NCHW) output mapping.
+// stores with the GEMM (row-major) or conv (NCHW or NCHW4) output mapping.
 // POOL (pooled conv): one thread per pool window (4 consecutive columns of
 // a tile), max of the 4 finished values in window order.
 template <int BM, int BN, bool CONV, bool POOL = false>
@@ -748,7 +778,7 @@ __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles
         if (g.flags & CAMEL_EPI_RELU) s = relu_idiom(s);
         if constexpr (CONV) {
             const int img = col / g.P, p = col - img * g.P;
-            g.C[((size_t)img * g.M + row) * g.P + p] = s;
+            g.C[conv_out_off(g, (g.flags & CAMEL_CONV_Y_NCHW4) != 0, img, row, p)] = s;
         } else {
             g.C[(size_t)row * g.ldc + col] = s;
         }
@@ -1169,6 +1199,32 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_kernel(const float *__restri
     }
 }
 
+// NCHW <-> NCHW4 ([N][C/4][H][W][4], C % 4 == 0) over `quads` = N*C/4
+// channel quads of HW pixels.  Thread = (channel quad, pixel): on the NCHW
+// side four scalar accesses one plane apart (each coalesced over a wave's
+// consecutive pixels), on the NCHW4 side one 16-byte access.
+template <bool TO_Q4>
+__global__ __launch_bounds__(256) void quad_layout_kernel(const float *__restrict__ src,
+                                                          float *__restrict__ dst, int64_t quads,
+                                                          int HW) {
+    const int64_t total = quads * HW, step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        const int64_t q = i / HW;
+        const size_t plane = (size_t)(4 * q) * HW + (size_t)(i - q * HW);
+        if constexpr (TO_Q4) {
+            reinterpret_cast<float4 *>(dst)[i] =
+                make_float4(src[plane], src[plane + HW], src[plane + 2 * (size_t)HW],
+                            src[plane + 3 * (size_t)HW]);
+        } else {
+            const float4 v = reinterpret_cast<const float4 *>(src)[i];
+            dst[plane] = v.x;
+            dst[plane + HW] = v.y;
+            dst[plane + 2 * (size_t)HW] = v.z;
+            dst[plane + 3 * (size_t)HW] = v.w;
+        }
+    }
+}
+
 // Direct convolution for a tiny reduction (C*KH*KW <= DIRECT_MAX_K, e.g. the
 // first layer of an image CNN with C = 1): one thread per output pixel, all
 // output channels.  The patch is loaded once into registers; the weights are
@@ -1185,7 +1241,11 @@ constexpr int DIRECT_MAX_K = 32;
 // around a lone scalar load and its full latency).
 // PIX consecutive output pixels per thread (P % PIX == 0, so they share an
 // image): the channel loop then stores PIX-wide vectors.
-template <int KMAX, bool EXACT, int PIX>
+// Q4: y is NCHW4 ([N][Co/4][OH][OW][4], Co % 4 == 0, 16-byte aligned); the
+// channel loop runs a channel quad at a time and stores one 16-byte vector
+// per pixel, consecutive lanes on consecutive pixels (the same values as the
+// NCHW variant: each output is the same FMA chain).
+template <int KMAX, bool EXACT, int PIX, bool Q4 = false>
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(
     const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ bias,
     float *__restrict__ y, int NP, int P, int OW, int C, int H, int W, int Co, int KH, int KW,
@@ -1220,10 +1280,33 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
             xv[j][k] = v;
         }
     }
-    float *yo = y + (size_t)img * Co * P + p;
+    float *yo = y + (size_t)img * Co * P + (Q4 ? 4 * (size_t)p : p);
     // Epilogue flags are fixed per variant so the channel loop has no
     // branches and its scalar loads batch across unrolled channels.
     auto channels = [&](auto has_bias, auto has_relu) {
+        if constexpr (Q4) {
+            for (int co = 0; co < Co; co += 4) {
+                float4 out[PIX];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float *wr = w + (size_t)(co + r) * K;
+#pragma unroll
+                    for (int j = 0; j < PIX; ++j) {
+                        float acc = 0.f;
+#pragma unroll
+                        for (int k = 0; k < KMAX; ++k)
+                            if (EXACT || k < K) acc = __builtin_fmaf(wr[k], xv[j][k], acc);
+                        if constexpr (decltype(has_bias)::value) acc = acc + bias[co + r];
+                        if constexpr (decltype(has_relu)::value) acc = relu_idiom(acc);
+                        out[j][r] = acc;
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < PIX; ++j)
+                    *reinterpret_cast<float4 *>(yo + (size_t)co * P + 4 * j) = out[j];
+            }
+            return;
+        }
 #pragma unroll 4
         for (int co = 0; co < Co; ++co) {
             const float *wr = w + (size_t)co * K;
@@ -1557,12 +1640,16 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
 
 // ---- conv2d host paths -----------------------------------------------------------
 
+// Activation layouts of the conv paths: NCHW (the tensor layout), NHWC and
+// NCHW4 ([N][C/4][H][W][4]), the last two chosen by the layout flags.
+enum Layout { L_NCHW, L_NHWC, L_NCHW4 };
+
 int conv2d_direct(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
                   int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
-                  int64_t pad, int64_t OH, int64_t OW, int flags, bool y_nhwc) {
+                  int64_t pad, int64_t OH, int64_t OW, int flags, Layout y_layout) {
     const int64_t P = OH * OW, NP = N * P;
     const int64_t K = C * KH * KW;
-    if (y_nhwc) {
+    if (y_layout == L_NHWC) {
         // Co % 4 == 0 and y 16-byte aligned (checked by the caller)
         auto go = [&](auto kernel) {
             hipLaunchKernelGGL(kernel, dim3((unsigned)((NP + DN_PIX - 1) / DN_PIX)), dim3(DN_PIX), 0, stream(),
@@ -1587,6 +1674,20 @@ int conv2d_direct(const float *x, const float *w, const float *bias, float *y, i
                            (int)KH, (int)KW, (int)stride, (int)pad, flags);
         return check_launch("conv2d_direct_kernel");
     };
+    if (y_layout == L_NCHW4) {
+        // Co % 4 == 0 and y 16-byte aligned (checked by the caller)
+        if (K == 9)
+            return pair ? go(conv2d_direct_kernel<9, true, 2, true>, 2)
+                        : go(conv2d_direct_kernel<9, true, 1, true>, 1);
+        if (K == 25)
+            return pair ? go(conv2d_direct_kernel<25, true, 2, true>, 2)
+                        : go(conv2d_direct_kernel<25, true, 1, true>, 1);
+        if (K == 27)
+            return pair ? go(conv2d_direct_kernel<27, true, 2, true>, 2)
+                        : go(conv2d_direct_kernel<27, true, 1, true>, 1);
+        if (K <= 16) return go(conv2d_direct_kernel<16, false, 1, true>, 1);
+        return go(conv2d_direct_kernel<DIRECT_MAX_K, false, 1, true>, 1);
+    }
     // Exact kernels for the usual first layers: 3x3 and 5x5 over 1 or 3
     // channels.
     if (K == 9)
@@ -1620,6 +1721,20 @@ int transpose_images(const float *src, float *dst, int64_t N, int64_t A, int64_t
         hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, grid, dim3(256), 0, stream(), src, dst,
                            (int)A, (int)B, nullptr, nullptr, 0, 1);
     return check_launch("nchw_to_nhwc_kernel");
+}
+
+// NCHW -> NCHW4 (to_q4) or back, for `quads` = N*C/4 channel quads of HW
+// pixels; the NCHW4 side 16-byte aligned.
+int quad_layout(const float *src, float *dst, int64_t quads, int64_t HW, bool to_q4) {
+    if (quads * HW == 0) return ok();
+    const dim3 grid(grid_for(quads * HW, 256));
+    if (to_q4)
+        hipLaunchKernelGGL(quad_layout_kernel<true>, grid, dim3(256), 0, stream(), src, dst, quads,
+                           (int)HW);
+    else
+        hipLaunchKernelGGL(quad_layout_kernel<false>, grid, dim3(256), 0, stream(), src, dst, quads,
+                           (int)HW);
+    return check_launch("quad_layout_kernel");
 }
 
 // w [Co][C][KHW] -> wp [Co][KHW][C] (the K order (kh, kw, c) of the NHWC
@@ -1666,18 +1781,22 @@ GemmArgs conv_args(const float *w, const float *x, const float *bias, float *y, 
     g.pad = (int)pad;
     g.Cin = (int)C;
     g.KW = (int)KW;
+    g.pxs = (int)C; // NHWC
+    g.cqs = 4;
     return g;
 }
 
-// NHWC implicit GEMM: x is transposed to NHWC (unless it already is) and w
-// reordered to (kh, kw, c) in pooled scratch (stream-ordered, returned to the
-// pool after the launch).  pool: y is the 2x2 stride-2 max pool of the
-// convolution, [N][Co][OH/2][OW/2], written from the GEMM epilogue.
+// NHWC implicit GEMM: an NCHW x is transposed to NHWC (NHWC and NCHW4 are
+// read in place) and w reordered to (kh, kw, c) in pooled scratch
+// (stream-ordered, returned to the pool after the launch).  pool: y is the
+// 2x2 stride-2 max pool of the convolution, [N][Co][OH/2][OW/2], written from
+// the GEMM epilogue.
 template <class T>
 int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
                 int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
-                int64_t pad, int64_t OH, int64_t OW, int flags, bool x_nhwc, bool pool,
+                int64_t pad, int64_t OH, int64_t OW, int flags, Layout x_layout, bool pool,
                 bool w_packed) {
+    const bool in_place = x_layout != L_NCHW;
     const int64_t HW = H * W, K = C * KH * KW;
     Scratch xt, wt;
     // packed weights (already (kh, kw, c)): nothing to reorder; the
@@ -1685,7 +1804,7 @@ int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int
     const int64_t co_reorder = w_packed ? 0 : Co;
     if (!w_packed) CAMEL_RETURN_IF(wt.alloc((size_t)(Co * K) * sizeof(float)));
     const float *wk = w_packed ? w : wt.f();
-    if (!x_nhwc) {
+    if (!in_place) {
         CAMEL_RETURN_IF(xt.alloc((size_t)(N * C * HW) * sizeof(float)));
         // xt comes from the pool (256-byte aligned); x is 16-byte aligned here.
         const bool vec = HW % 4 == 0 && C % 4 == 0;
@@ -1701,8 +1820,12 @@ int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int
     } else if (!w_packed) {
         CAMEL_RETURN_IF(pack_weights(w, wt.f(), Co, C, KH * KW));
     }
-    GemmArgs g = conv_args(wk, x_nhwc ? x : xt.f(), bias, y, N, C, H, W, Co, KH, KW, stride, pad,
+    GemmArgs g = conv_args(wk, in_place ? x : xt.f(), bias, y, N, C, H, W, Co, KH, KW, stride, pad,
                            OH, OW, flags);
+    if (x_layout == L_NCHW4) {
+        g.pxs = 4;
+        g.cqs = (int)(4 * HW);
+    }
     if (pool) {
         g.PW = (int)(OW / 2);
         g.PP = (int)((OH / 2) * (OW / 2));
@@ -1779,25 +1902,39 @@ int conv_check(const float *x, const float *w, const float *bias, const float *y
     if (N * C * H * W > INT32_MAX || NP > INT32_MAX || N * Co * P > INT32_MAX || Co * K > INT32_MAX)
         return fail(CAMEL_HIP_ERR_SHAPE, name + ": tensor too large");
     if (flags & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU | CAMEL_CONV_X_NHWC | CAMEL_CONV_Y_NHWC |
-                  CAMEL_CONV_W_PACKED))
+                  CAMEL_CONV_W_PACKED | CAMEL_CONV_X_NCHW4 | CAMEL_CONV_Y_NCHW4))
         return fail(CAMEL_HIP_ERR_ARG, name + ": unknown flags");
+    if ((flags & CAMEL_CONV_X_NHWC) && (flags & CAMEL_CONV_X_NCHW4))
+        return fail(CAMEL_HIP_ERR_ARG, name + ": two input layouts");
+    if ((flags & CAMEL_CONV_Y_NHWC) && (flags & CAMEL_CONV_Y_NCHW4))
+        return fail(CAMEL_HIP_ERR_ARG, name + ": two output layouts");
+    if ((flags & CAMEL_CONV_X_NCHW4) && (C % 4 != 0 || ((uintptr_t)x & 15) != 0))
+        return fail(CAMEL_HIP_ERR_ARG, name + ": an NCHW4 input needs C % 4 == 0 and 16-byte alignment");
+    if ((flags & CAMEL_CONV_Y_NCHW4) && (Co % 4 != 0 || ((uintptr_t)y & 15) != 0))
+        return fail(CAMEL_HIP_ERR_ARG, name + ": an NCHW4 output needs Co % 4 == 0 and 16-byte alignment");
     if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, name + ": null bias");
     if (N > 0 && (!x || !w || !y)) return fail(CAMEL_HIP_ERR_ARG, name + ": null operand");
     return CAMEL_HIP_OK;
 }
 
 // Every conv2d runs here.  The NHWC implicit GEMM serves C % 16 == 0 and
-// reads an NHWC input in place; the direct kernel serves C*KH*KW <= 32 and
-// can write NHWC; every other layout combination goes through transposes
-// into pooled scratch, so all of them compute the same values.  pool: y is
-// the 2x2 stride-2 max pool of the result (from the GEMM epilogue when the
-// NHWC GEMM serves the shape, else a pool pass over a scratch result).
+// reads an NHWC or NCHW4 input in place; the direct kernel serves
+// C*KH*KW <= 32 and writes NHWC or NCHW4 directly; every other layout
+// combination goes through conversions into pooled scratch, so all of them
+// compute the same values.  pool: y is the 2x2 stride-2 max pool of the
+// result (from the GEMM epilogue when the NHWC GEMM serves the shape, else a
+// pool pass over a scratch result).
 int conv2d_run(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
                int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
                int flags, bool pool) {
     const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
     const int64_t K = C * KH * KW, HW = H * W, P = OH * OW;
-    const bool x_nhwc = (flags & CAMEL_CONV_X_NHWC) != 0, y_nhwc = (flags & CAMEL_CONV_Y_NHWC) != 0;
+    const Layout xl = (flags & CAMEL_CONV_X_NHWC)    ? L_NHWC
+                      : (flags & CAMEL_CONV_X_NCHW4) ? L_NCHW4
+                                                     : L_NCHW;
+    const Layout yl = (flags & CAMEL_CONV_Y_NHWC)    ? L_NHWC
+                      : (flags & CAMEL_CONV_Y_NCHW4) ? L_NCHW4
+                                                     : L_NCHW;
     const int epi = flags & (CAMEL_EPI_BIAS | CAMEL_EPI_RELU);
     const bool aligned = (((uintptr_t)x | (uintptr_t)w) & 15) == 0;
     // (the NCHW -> NHWC transpose runs one image per grid z, plus one z for
@@ -1813,53 +1950,66 @@ int conv2d_run(const float *x, const float *w, const float *bias, float *y, int6
         w_packed = false;
         flags &= ~CAMEL_CONV_W_PACKED;
     }
-    auto nhwc_gemm = [&](float *out, bool pooled) -> int {
+    // out_flags: the epilogue flags, plus CAMEL_CONV_Y_NCHW4 for an NCHW4 out
+    auto nhwc_gemm = [&](float *out, bool pooled, int out_flags) -> int {
         const bool k32 = C % 32 == 0;
         if (Co > 64)
             return k32 ? conv2d_nhwc<TileConv>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH,
-                                              OW, epi, x_nhwc, pooled, w_packed)
+                                              OW, out_flags, xl, pooled, w_packed)
                        : conv2d_nhwc<TileConv16>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad,
-                                                OH, OW, epi, x_nhwc, pooled, w_packed);
+                                                OH, OW, out_flags, xl, pooled, w_packed);
         return k32 ? conv2d_nhwc<TileConv64>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH,
-                                            OW, epi, x_nhwc, pooled, w_packed)
+                                            OW, out_flags, xl, pooled, w_packed)
                    : conv2d_nhwc<TileConv64k16>(x, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad,
-                                               OH, OW, epi, x_nhwc, pooled, w_packed);
+                                               OH, OW, out_flags, xl, pooled, w_packed);
     };
     if (pool) {
-        if (gemm_nhwc) return nhwc_gemm(y, true);
+        if (gemm_nhwc) return nhwc_gemm(y, true, epi);
         Scratch full;
         CAMEL_RETURN_IF(full.alloc((size_t)(N * Co * P) * sizeof(float)));
         CAMEL_RETURN_IF(conv2d_run(x, w, bias, full.f(), N, C, H, W, Co, KH, KW, stride, pad,
-                                   flags & ~CAMEL_CONV_Y_NHWC, false));
+                                   flags & ~(CAMEL_CONV_Y_NHWC | CAMEL_CONV_Y_NCHW4), false));
         return camel_hip_maxpool2d(full.f(), y, N, Co, OH, OW, 2, 2, 2);
     }
-    // NCHW result into y, or into scratch that is then transposed to NHWC.
+    // The result in y's layout straight from the kernel (NCHW; NCHW4 from
+    // the direct kernel and the implicit GEMM; NHWC from the direct kernel),
+    // or NCHW into scratch that is then converted.
     const bool direct = K <= DIRECT_MAX_K;
-    const bool direct_nhwc_out = direct && y_nhwc && Co % 4 == 0 && ((uintptr_t)y & 15) == 0;
+    const bool native_out =
+        yl == L_NCHW || (yl == L_NCHW4 && (direct || gemm_nhwc)) ||
+        (yl == L_NHWC && direct && Co % 4 == 0 && ((uintptr_t)y & 15) == 0);
     Scratch ytmp;
     float *out = y;
-    if (y_nhwc && !direct_nhwc_out) {
+    if (!native_out) {
         CAMEL_RETURN_IF(ytmp.alloc((size_t)(N * Co * P) * sizeof(float)));
         out = ytmp.f();
     }
     if (gemm_nhwc) {
-        CAMEL_RETURN_IF(nhwc_gemm(out, false));
+        CAMEL_RETURN_IF(nhwc_gemm(out, false, epi | (out == y && yl == L_NCHW4 ? CAMEL_CONV_Y_NCHW4 : 0)));
     } else {
         Scratch xtmp;
         const float *xs = x;
-        if (x_nhwc) {
+        if (xl != L_NCHW) {
             CAMEL_RETURN_IF(xtmp.alloc((size_t)(N * C * HW) * sizeof(float)));
-            CAMEL_RETURN_IF(transpose_images(x, xtmp.f(), N, HW, C));
+            if (xl == L_NHWC)
+                CAMEL_RETURN_IF(transpose_images(x, xtmp.f(), N, HW, C));
+            else
+                CAMEL_RETURN_IF(quad_layout(x, xtmp.f(), N * C / 4, HW, false));
             xs = xtmp.f();
         }
         if (direct)
             CAMEL_RETURN_IF(conv2d_direct(xs, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH, OW,
-                                          epi, direct_nhwc_out));
+                                          epi, out == y ? yl : L_NCHW));
         else
             CAMEL_RETURN_IF(conv2d_gather(xs, w, bias, out, N, C, H, W, Co, KH, KW, stride, pad, OH, OW,
                                           epi));
     }
-    if (out != y) CAMEL_RETURN_IF(transpose_images(out, y, N, Co, P));
+    if (out != y) {
+        if (yl == L_NHWC)
+            CAMEL_RETURN_IF(transpose_images(out, y, N, Co, P));
+        else
+            CAMEL_RETURN_IF(quad_layout(out, y, N * Co / 4, P, true));
+    }
     return CAMEL_HIP_OK;
 }
 
@@ -1988,7 +2138,7 @@ int camel_hip_conv2d_pool2(const float *x, const float *w, const float *bias, fl
                            int64_t stride, int64_t pad, int flags) {
     CAMEL_RETURN_IF(
         conv_check(x, w, bias, y, N, C, H, W, Co, KH, KW, stride, pad, flags, "conv2d_pool2"));
-    if (flags & CAMEL_CONV_Y_NHWC)
+    if (flags & (CAMEL_CONV_Y_NHWC | CAMEL_CONV_Y_NCHW4))
         return fail(CAMEL_HIP_ERR_ARG, "conv2d_pool2: the pooled output is NCHW only");
     const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
     if (OH < 2 || OW < 2) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d_pool2: window larger than input");

@@ -16,11 +16,11 @@ std::string stripPrefix(const std::string &name) {
     return name.rfind("tensor:", 0) == 0 ? name.substr(7) : name;
 }
 
-// The NHWC implicit GEMM of libcamel_hip reads an NHWC input in place when
-// C % 16 == 0 and C*KH*KW exceeds the direct kernel's 32 (its transpose runs
-// one image per grid z, so the batch stays below 65535).  Only then is an
-// NHWC intermediate worth writing.
-bool readsNhwc(const LayerStep &conv, int64_t batch) {
+// The implicit GEMM of libcamel_hip reads an NCHW4 input in place when
+// C % 16 == 0 and C*KH*KW exceeds the direct kernel's 32 (for an NCHW input
+// its transpose runs one image per grid z, so the batch stays below 65535).
+// Only then is an NCHW4 intermediate worth writing.
+bool readsInPlace(const LayerStep &conv, int64_t batch) {
     const int64_t C = conv.w->dim(1), KH = conv.w->dim(2), KW = conv.w->dim(3);
     return C % 16 == 0 && C * KH * KW > 32 && batch < 65535;
 }
@@ -29,12 +29,13 @@ int64_t intOr(const LayerStep &s, size_t i, int64_t fallback) {
     return i < s.ints.size() ? s.ints[i] : fallback;
 }
 
-// A device activation between two groups: a tensor, or an NHWC buffer of the
-// logical NCHW shape `shape` that only a conv reads.
+// A device activation between two groups: a tensor, or an NCHW4 buffer
+// ([N][C/4][H][W][4]) of the logical NCHW shape `shape` that only a conv
+// reads.
 struct Activation {
     const TensorObject *tensor = nullptr;
     bool owned = false;
-    void *nhwc = nullptr;
+    void *nchw4 = nullptr;
     std::vector<int64_t> shape;
 
     Activation() = default;
@@ -46,21 +47,21 @@ struct Activation {
             reset();
             tensor = o.tensor;
             owned = o.owned;
-            nhwc = o.nhwc;
+            nchw4 = o.nchw4;
             shape = std::move(o.shape);
             o.tensor = nullptr;
             o.owned = false;
-            o.nhwc = nullptr;
+            o.nchw4 = nullptr;
         }
         return *this;
     }
     ~Activation() { reset(); }
     void reset() {
         if (owned && tensor) releaseTensor(const_cast<TensorObject *>(tensor));
-        if (nhwc) camel_hip_free(nhwc);
+        if (nchw4) camel_hip_free(nchw4);
         tensor = nullptr;
         owned = false;
-        nhwc = nullptr;
+        nchw4 = nullptr;
     }
     static Activation of(TensorObject *t) {
         Activation a;
@@ -140,7 +141,7 @@ const void *LayerChain::packedWeights(size_t i) const {
 std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> shape) const {
     std::vector<Group> groups;
     // Batch of the current activation where it is known (rank-4 shapes are
-    // propagated through conv / pool / relu; anything else stops NHWC
+    // propagated through conv / pool / relu; anything else stops NCHW4
     // pairing, which only changes speed, never values).
     int64_t batch = shape.size() == 4 ? shape[0] : -1;
     const size_t n = steps_.size();
@@ -175,10 +176,11 @@ std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> sha
                 g.pool = true;
                 ++j;
             }
-            g.x_nhwc = !groups.empty() && groups.back().kind == Group::Conv && groups.back().y_nhwc;
-            g.w_packed = batch >= 0 && readsNhwc(s, batch);
-            g.y_nhwc = !g.pool && j < n && steps_[j].kind == LayerKind::Conv2d && batch >= 0 &&
-                       readsNhwc(steps_[j], batch);
+            g.x_nchw4 = !groups.empty() && groups.back().kind == Group::Conv && groups.back().y_nchw4;
+            g.w_packed = batch >= 0 && readsInPlace(s, batch);
+            g.y_nchw4 = !g.pool && s.w->dim(0) % 4 == 0 && j < n &&
+                        steps_[j].kind == LayerKind::Conv2d && batch >= 0 &&
+                        readsInPlace(steps_[j], batch);
             break;
         case LayerKind::Relu:
             g.kind = Group::Relu;
@@ -215,8 +217,8 @@ std::string LayerChain::plan(std::span<const int64_t> shape) const {
         case Group::Conv:
             out << (g.relu ? "conv2d_relu" : "conv2d");
             if (g.pool) out << "+maxpool2d(2,2)";
-            if (g.x_nhwc) out << " x=nhwc";
-            if (g.y_nhwc) out << " y=nhwc";
+            if (g.x_nchw4) out << " x=nchw4";
+            if (g.y_nchw4) out << " y=nchw4";
             break;
         case Group::Relu:
             out << "relu";
@@ -272,7 +274,7 @@ TensorObject *LayerChain::apply(const TensorObject *x) const {
             break;
         case Group::Conv: {
             const int64_t stride = intOr(s, 0, 1), pad = intOr(s, 1, 0);
-            const TypeCode xdt = cur.nhwc ? TypeCode::Float32 : cur.tensor->dtype();
+            const TypeCode xdt = cur.nchw4 ? TypeCode::Float32 : cur.tensor->dtype();
             auto os = conv2dOutputShape(cur.shape, xdt, s.w, s.bias, stride, pad);
             if (g.pool) {
                 if (os[2] < 2 || os[3] < 2)
@@ -282,17 +284,18 @@ TensorObject *LayerChain::apply(const TensorObject *x) const {
             }
             const int64_t numel = os[0] * os[1] * os[2] * os[3];
             void *y;
-            if (g.y_nhwc) {
+            if (g.y_nchw4) {
                 next.shape.assign(os.begin(), os.end());
-                checkHip(camel_hip_malloc(&next.nhwc, (size_t)std::max<int64_t>(numel, 1) * 4));
-                y = next.nhwc;
+                checkHip(camel_hip_malloc(&next.nchw4, (size_t)std::max<int64_t>(numel, 1) * 4));
+                y = next.nchw4;
             } else {
                 next = Activation::of(TensorObject::create(TypeCode::Float32, os, Residence::Device));
                 y = numel > 0 ? const_cast<TensorObject *>(next.tensor)->deviceOutput() : nullptr;
             }
             if (numel > 0) {
-                const void *xin = cur.nhwc ? cur.nhwc : cur.tensor->deviceData();
-                const int layout = (g.x_nhwc ? CAMEL_CONV_X_NHWC : 0) | (g.y_nhwc ? CAMEL_CONV_Y_NHWC : 0);
+                const void *xin = cur.nchw4 ? cur.nchw4 : cur.tensor->deviceData();
+                const int layout =
+                    (g.x_nchw4 ? CAMEL_CONV_X_NCHW4 : 0) | (g.y_nchw4 ? CAMEL_CONV_Y_NCHW4 : 0);
                 const void *wp = g.w_packed ? packedWeights((size_t)(&s - steps_.data())) : nullptr;
                 conv2dLaunch(xin, cur.shape, s.w, s.bias, stride, pad, g.relu, g.pool, layout, y, wp);
             }
@@ -301,7 +304,7 @@ TensorObject *LayerChain::apply(const TensorObject *x) const {
         }
         cur = std::move(next);
     }
-    if (cur.nhwc) throw std::logic_error("chain ended on an NHWC intermediate");
+    if (cur.nchw4) throw std::logic_error("chain ended on an NCHW4 intermediate");
     if (!cur.owned) {
         // an empty chain: x -> x is a new tensor with the same payload
         return tensorReshape(cur.tensor, cur.shape);

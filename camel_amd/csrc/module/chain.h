@@ -9,9 +9,10 @@
 //                                        conv2d_relu)
 //   dense (+relu) + softmax           -> camel_hip_dense_softmax
 //   conv2d (+relu) + maxpool2d(2, 2)  -> camel_hip_conv2d_pool2
-//   conv2d -> conv2d that reads NHWC  -> the first writes NHWC and the second
+//   conv2d -> conv2d that reads NCHW4 -> the first writes NCHW4
+//                                        ([N][C/4][H][W][4]) and the second
 //                                        reads it in place (no transpose)
-// A conv2d that runs as the NHWC implicit GEMM gets its weights packed once
+// A conv2d that runs as the implicit GEMM gets its weights packed once
 // per chain (camel_hip_conv2d_pack_weights) instead of once per call.
 // Every group's values equal the layer-by-layer operators' bit for bit,
 // except conv2d + maxpool2d where the partial last round of a large
@@ -59,7 +60,7 @@ public:
     // text.
     TensorObject *apply(const TensorObject *x) const;
     // The kernel groups apply would run for an input of this shape, one per
-    // line (e.g. "conv2d_relu+maxpool2d(2,2) x=nhwc").
+    // line (e.g. "conv2d_relu+maxpool2d(2,2) x=nchw4").
     std::string plan(std::span<const int64_t> shape) const;
     size_t size() const { return steps_.size(); }
 
@@ -69,9 +70,9 @@ private:
         const LayerStep *step; // first layer of the group
         bool relu = false;
         bool pool = false;     // conv + maxpool2d(2, 2)
-        bool x_nhwc = false;   // conv input comes NHWC from the previous conv
-        bool y_nhwc = false;   // conv output goes NHWC to the next conv
-        bool w_packed = false; // conv runs as the NHWC GEMM: weights packed once
+        bool x_nchw4 = false;  // conv input comes NCHW4 from the previous conv
+        bool y_nchw4 = false;  // conv output goes NCHW4 to the next conv
+        bool w_packed = false; // conv runs as the implicit GEMM: weights packed once
     };
     std::vector<Group> schedule(std::span<const int64_t> shape) const;
     // The packed form of step i's conv weights (made on first use; tensors

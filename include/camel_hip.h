@@ -57,11 +57,16 @@ enum camel_hip_epilogue { CAMEL_EPI_NONE = 0, CAMEL_EPI_BIAS = 1, CAMEL_EPI_RELU
 /* Layout bits of the conv2d flags, for a fused layer chain that keeps an
  * intermediate in the layout its consumer reads: x given as [N, H, W, C],
  * y written as [N, OH, OW, Co], w given as [Co, KH, KW, C] (packed once by
- * camel_hip_conv2d_pack_weights).  Each is only an addressing change. */
+ * camel_hip_conv2d_pack_weights), x given / y written as NCHW4
+ * [N, C/4, H, W, 4] (channel quads interleaved: C % 4 == 0 and 16-byte
+ * alignment; at most one input and one output layout bit).  Each is only
+ * an addressing change. */
 enum camel_hip_conv_layout {
     CAMEL_CONV_X_NHWC = 0x100,
     CAMEL_CONV_Y_NHWC = 0x200,
-    CAMEL_CONV_W_PACKED = 0x400
+    CAMEL_CONV_W_PACKED = 0x400,
+    CAMEL_CONV_X_NCHW4 = 0x800,
+    CAMEL_CONV_Y_NCHW4 = 0x1000
 };
 
 /* ---- runtime ------------------------------------------------------------- */
@@ -130,8 +135,8 @@ int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int
 /* ---- conv2d / pooling (no reference op; defined by composition) --------- */
 /* y[N,Co,OH,OW] = conv(x[N,C,H,W], w[Co,C,KH,KW]) (+bias[Co]) (relu), NCHW,
  * implicit GEMM on the same MFMA core.  OH = (H+2*pad-KH)/stride+1.
- * flags may add CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC / CAMEL_CONV_W_PACKED
- * (same values, other addressing). */
+ * flags may add the camel_hip_conv_layout bits (same values, other
+ * addressing). */
 int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y, int64_t N,
                      int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
                      int64_t stride, int64_t pad, int flags);
@@ -146,7 +151,7 @@ int camel_hip_conv2d_pack_weights(const float *w, float *wp, int64_t Co, int64_t
  * camel_hip_maxpool2d) is taken in the convolution's epilogue, so the
  * full-size result never reaches HBM.  No reference operator (compose is a
  * stub, src/builtin/operators/macro.cpp:30).  flags may add
- * CAMEL_CONV_X_NHWC / CAMEL_CONV_W_PACKED; OH, OW >= 2. */
+ * CAMEL_CONV_X_NHWC / CAMEL_CONV_X_NCHW4 / CAMEL_CONV_W_PACKED; OH, OW >= 2. */
 int camel_hip_conv2d_pool2(const float *x, const float *w, const float *bias, float *y, int64_t N,
                            int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
                            int64_t stride, int64_t pad, int flags);

@@ -28,10 +28,10 @@ def cnn_chain(c1=1, c2=32, c3=64):
 
 
 def test_cnn_chain_plan_fuses_every_pair():
-    # The benchmark small CNN as a chain: conv1 writes NHWC for conv2, conv2 + relu
+    # The benchmark small CNN as a chain: conv1 writes NCHW4 for conv2, conv2 + relu
     # + pool are one kernel, the classifier and the softmax one more.
     assert cnn_chain().plan((512, 1, 28, 28)) == [
-        "conv2d_relu y=nhwc", "conv2d_relu+maxpool2d(2,2) x=nhwc", "reshape", "dense_relu",
+        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4", "reshape", "dense_relu",
         "dense+softmax"]
 
 
@@ -48,16 +48,20 @@ W = "w"  # a weight tensor of the given shape, made inside the test
 
 
 @pytest.mark.parametrize("layers,shape,plan", [
-    # consumer with C % 16 != 0 takes the NCHW gather path: no NHWC intermediate
+    # consumer with C % 16 != 0 takes the NCHW gather path: no NCHW4 intermediate
     ([("conv2d", (W, 12, 3, 3, 3)), ("conv2d", (W, 8, 12, 3, 3))], (2, 3, 9, 9),
      ["conv2d", "conv2d"]),
     # consumer 1x1 over 16 channels is a direct conv (K = 16 <= 32): NCHW
     ([("conv2d", (W, 16, 1, 3, 3)), ("conv2d", (W, 8, 16, 1, 1))], (2, 1, 9, 9),
      ["conv2d", "conv2d"]),
-    # a relu between two convs joins the first; three convs chain NHWC twice
+    # a relu between two convs joins the first; three convs chain NCHW4 twice
     ([("conv2d", (W, 32, 1, 3, 3)), "relu", ("conv2d", (W, 32, 32, 3, 3)),
       ("conv2d", (W, 16, 32, 3, 3))],
-     (2, 1, 12, 12), ["conv2d_relu y=nhwc", "conv2d x=nhwc y=nhwc", "conv2d x=nhwc"]),
+     (2, 1, 12, 12), ["conv2d_relu y=nchw4", "conv2d x=nchw4 y=nchw4", "conv2d x=nchw4"]),
+    # an NCHW4 intermediate needs the producer's Co % 4 == 0 (here 18: the
+    # consumer then fails on its channel count, as the layer call would)
+    ([("conv2d", (W, 18, 1, 3, 3)), ("conv2d", (W, 8, 16, 3, 3))], (2, 1, 9, 9),
+     ["conv2d", "conv2d"]),
     # a pool that is not 2x2 stride 2 stays its own kernel
     ([("conv2d_relu", (W, 16, 16, 3, 3)), ("maxpool2d", 3, 2)], (1, 16, 9, 9),
      ["conv2d_relu", "maxpool2d(3,2)"]),

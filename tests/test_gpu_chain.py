@@ -53,7 +53,7 @@ def test_mlp_chain_equals_layer_calls():
 
 
 def test_cnn_chain_equals_layer_calls():
-    # The benchmark small CNN at batch 16: NHWC intermediate, fused pool, fused softmax
+    # The benchmark small CNN at batch 16: NCHW4 intermediate, fused pool, fused softmax
     B = 16
     x = D.uniform(0x6100, (B, 1, 28, 28), 0.0, 1.0)
     w1 = t(D.normal(0x6101, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9))))
@@ -65,7 +65,7 @@ def test_cnn_chain_equals_layer_calls():
     chain = T.Chain(("conv2d_relu", w1, b1), ("conv2d_relu", w2, b2), ("maxpool2d", 2, 2),
                     ("reshape", B, 9216), ("dense_relu", w3, b3), ("dense", w4, b4), "softmax")
     assert chain.plan((B, 1, 28, 28)) == [
-        "conv2d_relu y=nhwc", "conv2d_relu+maxpool2d(2,2) x=nhwc", "reshape", "dense_relu",
+        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4", "reshape", "dense_relu",
         "dense+softmax"]
     xt = t(x)
     got = chain(xt)
@@ -81,7 +81,7 @@ def test_cnn_chain_equals_layer_calls():
 
 
 def test_conv_chain_with_padding_stride_and_three_convs():
-    # conv -> conv -> conv through two NHWC intermediates, then a 3x3 pool
+    # conv -> conv -> conv through two NCHW4 intermediates, then a 3x3 pool
     x = D.normal(0x6200, (3, 3, 20, 18))
     ws = [t(D.normal(0x6201, (32, 3, 3, 3)) * F(0.2)), t(D.normal(0x6202, (48, 32, 3, 3)) * F(0.06)),
           t(D.normal(0x6203, (16, 48, 1, 1)) * F(0.15))]
@@ -89,7 +89,7 @@ def test_conv_chain_with_padding_stride_and_three_convs():
     chain = T.Chain(("conv2d_relu", ws[0], bs[0], 1, 1), ("conv2d", ws[1], bs[1], 2, 1), "relu",
                     ("conv2d_relu", ws[2], bs[2]), ("maxpool2d", 3, 2))
     assert chain.plan((3, 3, 20, 18)) == [
-        "conv2d_relu y=nhwc", "conv2d_relu x=nhwc y=nhwc", "conv2d_relu x=nhwc", "maxpool2d(3,2)"]
+        "conv2d_relu y=nchw4", "conv2d_relu x=nchw4 y=nchw4", "conv2d_relu x=nchw4", "maxpool2d(3,2)"]
     xt = t(x)
     got = chain(xt)
     h = T.call("conv2d_relu", xt, with_=(ws[0], bs[0], 1, 1))
@@ -143,7 +143,7 @@ def test_chain_int64_dense_and_softmax_follow_the_composition():
     chain.release()
 
 
-def test_conv_chain_without_nhwc_consumer_and_empty_batch():
+def test_conv_chain_without_nchw4_consumer_and_empty_batch():
     # second conv has C % 16 != 0: NCHW between them; and a batch of 0
     w1 = t(D.normal(0x6500, (12, 3, 3, 3)) * F(0.2))
     w2 = t(D.normal(0x6501, (8, 12, 3, 3)) * F(0.1))

@@ -5,8 +5,9 @@ unfused device chain and the CPU oracle.
   equals camel_hip_sgemm then camel_hip_softmax_rows bit for bit where the
   fused path serves (N <= 32, one value per lane), and the softmax of the
   device GEMM result per the oracle.
-* conv2d layouts: CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC change addressing
-  only, so results equal the NCHW conv bit for bit.
+* conv2d layouts: CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC and
+  CAMEL_CONV_X_NCHW4 / CAMEL_CONV_Y_NCHW4 change addressing only, so results
+  equal the NCHW conv bit for bit.
 * conv2d..maxpool2d: camel_hip_conv2d_pool2 equals camel_hip_conv2d then
   camel_hip_maxpool2d(2, 2, 2) bit for bit when both run one launch of the
   same tile (every output then sums in the same order); the oracle bounds the
@@ -163,6 +164,120 @@ def test_conv2d_chain_in_nhwc_equals_nchw_chain():
     y, _ = _conv(K.host(h_nhwc, F, (6, 26, 26, 32)), w2, b2, (6, 32, 26, 26, 64, 3, 3, 1, 0),
                  epi | H.CONV_X_NHWC)
     np.testing.assert_array_equal(K.host(y, F, shape), K.host(y_ref, F, shape))
+
+
+def _nchw4(a):
+    """[N, C, H, W] -> NCHW4 [N, C/4, H, W, 4]."""
+    n, c, h, w = a.shape
+    return np.ascontiguousarray(a.reshape(n, c // 4, 4, h, w).transpose(0, 1, 3, 4, 2))
+
+
+def _from_nchw4(a):
+    n, q, h, w, _ = a.shape
+    return np.ascontiguousarray(a.transpose(0, 1, 4, 2, 3).reshape(n, 4 * q, h, w))
+
+
+NCHW4_GEOMS = GEOMS + [
+    (2, 3, 11, 11, 8, 3, 3, 1, 0),      # direct K = 27, odd P: one pixel per thread
+    (3, 1, 12, 12, 16, 5, 5, 1, 0),     # direct K = 25, even P: pixel pairs
+    (2, 1, 9, 9, 8, 4, 4, 1, 0),        # direct K = 16 (guarded k loop)
+    (2, 2, 9, 9, 12, 4, 4, 1, 1),       # direct K = 32
+    (2, 4, 10, 10, 20, 3, 3, 1, 1),     # NCHW4 input to the direct path (converted)
+    (2, 16, 9, 11, 132, 3, 3, 2, 1),    # implicit GEMM, NCHW4 out from partial row tiles
+]
+
+
+@pytest.mark.parametrize("geom", NCHW4_GEOMS)
+def test_conv2d_nchw4_layouts_change_addressing_only(geom):
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    x = D.normal(0x5480 + Cin, (N, Cin, H_, W_))
+    w = D.normal(0x5481 + Co, (Co, Cin, kh, kw)) * F(np.sqrt(2.0 / (kh * kw * Cin)))
+    b = D.uniform(0x5482, (Co,), -0.1, 0.1)
+    for epi in (H.EPI_BIAS | H.EPI_RELU, 0):
+        bb = b if epi else None
+        dref, shape = _conv(x, w, bb, geom, epi)
+        ref = K.host(dref, F, shape)
+        q4 = (shape[0], shape[1] // 4, shape[2], shape[3], 4)
+        if Cin % 4 == 0:
+            dy, _ = _conv(_nchw4(x), w, bb, geom, epi | H.CONV_X_NCHW4)
+            np.testing.assert_array_equal(K.host(dy, F, shape), ref)
+        if Co % 4 == 0:
+            dy, _ = _conv(x, w, bb, geom, epi | H.CONV_Y_NCHW4)
+            np.testing.assert_array_equal(_from_nchw4(K.host(dy, F, q4)), ref)
+        if Cin % 4 == 0 and Co % 4 == 0:
+            dy, _ = _conv(_nchw4(x), w, bb, geom, epi | H.CONV_X_NCHW4 | H.CONV_Y_NCHW4)
+            np.testing.assert_array_equal(_from_nchw4(K.host(dy, F, q4)), ref)
+            # NCHW4 in, NHWC out and the reverse
+            dy, _ = _conv(_nchw4(x), w, bb, geom, epi | H.CONV_X_NCHW4 | H.CONV_Y_NHWC)
+            np.testing.assert_array_equal(K.host(dy, F, (shape[0], shape[2], shape[3], shape[1])),
+                                          ref.transpose(0, 2, 3, 1))
+            dy, _ = _conv(np.ascontiguousarray(x.transpose(0, 2, 3, 1)), w, bb, geom,
+                          epi | H.CONV_X_NHWC | H.CONV_Y_NCHW4)
+            np.testing.assert_array_equal(_from_nchw4(K.host(dy, F, q4)), ref)
+
+
+def test_conv2d_nchw4_output_from_whole_rounds_and_split_tails():
+    # enough tiles for whole rounds plus a K-split tail: the GEMM epilogue's
+    # 16-byte NCHW4 stores and the split reduce's NCHW4 addressing
+    geom = (32, 64, 56, 56, 128, 3, 3, 1, 1)
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    x = D.normal(0x5490, (N, Cin, H_, W_))
+    w = D.normal(0x5491, (Co, Cin, kh, kw)) * F(np.sqrt(2.0 / (kh * kw * Cin)))
+    b = D.uniform(0x5492, (Co,), -0.1, 0.1)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    dref, shape = _conv(x, w, b, geom, epi)
+    dy, _ = _conv(x, w, b, geom, epi | H.CONV_Y_NCHW4)
+    got = K.host(dy, F, (shape[0], shape[1] // 4, shape[2], shape[3], 4))
+    np.testing.assert_array_equal(_from_nchw4(got), K.host(dref, F, shape))
+
+
+def test_conv2d_chain_in_nchw4_equals_nchw_chain():
+    # CNN conv1 (direct) writing NCHW4 straight into conv2 (implicit GEMM)
+    # reading it in place, with packed weights, plain and pooled
+    x = D.uniform(0x5580, (6, 1, 28, 28), 0.0, 1.0)
+    w1 = D.normal(0x5581, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
+    w2 = D.normal(0x5582, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288)))
+    b1, b2 = D.uniform(0x5583, (32,), -0.1, 0.1), D.uniform(0x5584, (64,), -0.1, 0.1)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    g1, g2 = (6, 1, 28, 28, 32, 3, 3, 1, 0), (6, 32, 26, 26, 64, 3, 3, 1, 0)
+    h, _ = _conv(x, w1, b1, g1, epi)
+    hn = K.host(h, F, (6, 32, 26, 26))
+    y_ref, shape = _conv(hn, w2, b2, g2, epi)
+    p_ref, pshape = _conv(hn, w2, b2, g2, epi, pooled=True)
+    h4, _ = _conv(x, w1, b1, g1, epi | H.CONV_Y_NCHW4)
+    h4n = K.host(h4, F, (6, 8, 26, 26, 4))
+    np.testing.assert_array_equal(_from_nchw4(h4n), hn)
+    dw2, dwp = K.dev(w2), K.empty(w2.nbytes)
+    H.call("camel_hip_conv2d_pack_weights", P(dw2.ptr), P(dwp.ptr), 64, 32, 3, 3)
+    wp = K.host(dwp, F, (64, 3, 3, 32))
+    y, _ = _conv(h4n, wp, b2, g2, epi | H.CONV_X_NCHW4 | H.CONV_W_PACKED)
+    np.testing.assert_array_equal(K.host(y, F, shape), K.host(y_ref, F, shape))
+    py, _ = _conv(h4n, wp, b2, g2, epi | H.CONV_X_NCHW4 | H.CONV_W_PACKED, pooled=True)
+    np.testing.assert_array_equal(K.host(py, F, pshape), K.host(p_ref, F, pshape))
+
+
+def test_conv2d_nchw4_argument_errors():
+    lib = H.load()
+    d = K.empty(4 * 8 * 8 * 64)
+    ok = P(d.ptr)
+    off = P(d.ptr + 4)  # 4-byte aligned only
+    conv = lib.camel_hip_conv2d
+    # C % 4 != 0 / Co % 4 != 0
+    assert conv(ok, ok, None, ok, 1, 6, 8, 8, 8, 3, 3, 1, 0, H.CONV_X_NCHW4) == H.ERR_ARG
+    assert conv(ok, ok, None, ok, 1, 8, 8, 8, 6, 3, 3, 1, 0, H.CONV_Y_NCHW4) == H.ERR_ARG
+    # misaligned NCHW4 operands
+    assert conv(off, ok, None, ok, 1, 8, 8, 8, 8, 3, 3, 1, 0, H.CONV_X_NCHW4) == H.ERR_ARG
+    assert conv(ok, ok, None, off, 1, 8, 8, 8, 8, 3, 3, 1, 0, H.CONV_Y_NCHW4) == H.ERR_ARG
+    # two layouts for one operand
+    assert conv(ok, ok, None, ok, 1, 8, 8, 8, 8, 3, 3, 1, 0,
+                H.CONV_X_NCHW4 | H.CONV_X_NHWC) == H.ERR_ARG
+    assert conv(ok, ok, None, ok, 1, 8, 8, 8, 8, 3, 3, 1, 0,
+                H.CONV_Y_NCHW4 | H.CONV_Y_NHWC) == H.ERR_ARG
+    # the pooled output is NCHW only
+    assert lib.camel_hip_conv2d_pool2(ok, ok, None, ok, 1, 8, 8, 8, 8, 3, 3, 1, 0,
+                                      H.CONV_Y_NCHW4) == H.ERR_ARG
+    # nothing was launched on the error paths
+    H.sync()
 
 
 def test_conv2d_unknown_flags_rejected():
