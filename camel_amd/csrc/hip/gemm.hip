@@ -789,12 +789,22 @@ __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles
 // for an MFMA tile to be useful.  B [K, N] is staged in LDS zero-padded to
 // [256 * KV][NT] (NT >= N), so the inner loops run without guards; rows are
 // STRIDE = NT + 4 floats apart so that the eight lanes one 16-byte LDS read
-// serves per cycle land on disjoint banks.  Each wave owns one row of A at a
-// time: lane l takes k = l + 64 i (coalesced loads, zero past K) and
-// accumulates all NT columns in fp32 FMA; a wave-shuffle tree sums the 64
-// partials; bias and relu as in the MFMA epilogue.  SOFTMAX (the fused
+// serves per cycle land on disjoint banks.  Lanes take k = l + 64 i of a row
+// of A (coalesced loads, zero past K) and accumulate all NT columns in fp32
+// FMA; bias and relu as in the MFMA epilogue.  SOFTMAX (the fused
 // dense..softmax of a classifier) then takes the row softmax across the
 // wave's lanes, lane c holding column c, before the store.
+//   * N <= 16 (sgemm_thin_rows_kernel): 16-wave work-groups own 4 rows, and
+//     the 4 waves of a row take a quarter of the staged K each, so a CU
+//     holds 16 waves and B is staged with one batch of loads per thread.  A
+//     wave's 64 x NT partials meet in LDS (lane (c, s) adds the s-th segment
+//     of column c, then a shuffle tree over the segments), and the row's
+//     4 quarter sums are added in quarter order.  (One wave per row with a
+//     64-lane shuffle tree per column took 9.1 us at 1024 x 1024 -> 10 with
+//     the softmax; this takes 4.8 us.)
+//   * 16 < N <= 32 (sgemm_thin_kernel): one wave per row over all of K and a
+//     wave-shuffle tree per column (the 64 x 32 partials of 16 waves would
+//     not fit in LDS beside B).
 constexpr int THIN_LDS_FLOATS = 20480; // 80 KiB of B per work-group
 
 template <int NT, int KV, bool SOFTMAX = false>
@@ -872,6 +882,101 @@ __global__ __launch_bounds__(256) void sgemm_thin_kernel(const float *__restrict
     }
 }
 
+template <int NT, int KV, bool SOFTMAX = false>
+__global__ __launch_bounds__(1024) void sgemm_thin_rows_kernel(const float *__restrict__ A,
+                                                               const float *__restrict__ B,
+                                                               float *__restrict__ C, int M, int N,
+                                                               int K, const float *__restrict__ bias,
+                                                               int flags) {
+    constexpr int STRIDE = NT + 4, ROWS = 256 * KV, KQ = ROWS / 4, RS = NT + 1;
+    static_assert(NT == 8 || NT == 16, "partial segments assume 8 or 16 columns");
+    __shared__ __attribute__((aligned(16))) float bs[ROWS * STRIDE];
+    __shared__ float red[16][64 * RS]; // per wave: [lane][column], odd row stride
+    __shared__ float quarter[4][4][NT];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = wave >> 2, q = wave & 3; // row of the group, quarter of K
+    const int groups = (M + 3) / 4;
+    float av[KV];
+    auto load_a = [&](int grp) {
+        const int m = grp * 4 + r;
+#pragma unroll
+        for (int i = 0; i < KV; ++i) {
+            const int k = q * KQ + lane + 64 * i;
+            av[i] = (m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
+        }
+    };
+    int grp = blockIdx.x;
+    // The first group's A loads are in flight while B is staged (one batch of
+    // loads per thread, then the LDS stores).
+    load_a(grp);
+    constexpr int PER_THREAD = ROWS * NT / 1024;
+    float v[PER_THREAD];
+#pragma unroll
+    for (int u = 0; u < PER_THREAD; ++u) {
+        const int slot = u * 1024 + (int)threadIdx.x;
+        const int k = slot / NT, n = slot % NT;
+        v[u] = (k < K && n < N) ? B[(size_t)k * N + n] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < PER_THREAD; ++u) {
+        const int slot = u * 1024 + (int)threadIdx.x;
+        bs[(slot / NT) * STRIDE + slot % NT] = v[u];
+    }
+    __syncthreads();
+    float *rw = red[wave];
+    const int c = lane % NT, seg = lane / NT; // 64 / NT segments of NT lanes
+    for (; grp < groups; grp += gridDim.x) {
+        float acc[NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[n] = 0.f;
+#pragma unroll
+        for (int i = 0; i < KV; ++i) {
+            const float x = av[i];
+            const float4 *brow =
+                reinterpret_cast<const float4 *>(bs + (q * KQ + lane + 64 * i) * STRIDE);
+#pragma unroll
+            for (int c4 = 0; c4 < NT / 4; ++c4) {
+                const float4 bv = brow[c4];
+                acc[4 * c4 + 0] = __builtin_fmaf(x, bv.x, acc[4 * c4 + 0]);
+                acc[4 * c4 + 1] = __builtin_fmaf(x, bv.y, acc[4 * c4 + 1]);
+                acc[4 * c4 + 2] = __builtin_fmaf(x, bv.z, acc[4 * c4 + 2]);
+                acc[4 * c4 + 3] = __builtin_fmaf(x, bv.w, acc[4 * c4 + 3]);
+            }
+        }
+        // The next group's loads overlap this group's reduction.
+        if (grp + (int)gridDim.x < groups) load_a(grp + gridDim.x);
+        // The wave's partials: lane (c, seg) adds lanes seg*NT .. seg*NT+NT-1
+        // of column c (only this wave touches its slice, and a wave's LDS
+        // operations run in order), then the segments meet by shuffles.
+#pragma unroll
+        for (int n = 0; n < NT; ++n) rw[lane * RS + n] = acc[n];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) t += rw[(seg * NT + j) * RS + c];
+#pragma unroll
+        for (int off = NT; off < 64; off <<= 1) t += __shfl_xor(t, off);
+        if (lane < NT) quarter[r][q][lane] = t;
+        __syncthreads();
+        const int m = grp * 4 + r;
+        if (q == 0 && m < M) {
+            float out = 0.f;
+            if (lane < NT)
+                out = ((quarter[r][0][lane] + quarter[r][1][lane]) + quarter[r][2][lane]) +
+                      quarter[r][3][lane];
+            if (lane < N) {
+                if (flags & CAMEL_EPI_BIAS) out = out + bias[lane];
+                if (flags & CAMEL_EPI_RELU) out = relu_idiom(out);
+            }
+            if constexpr (SOFTMAX) out = softmax_row_lanes(lane < N ? out : -INFINITY);
+            if (lane < N) C[(size_t)m * N + lane] = out;
+        }
+        __syncthreads(); // quarter[] is rewritten by the next group
+    }
+}
+
 // True when the thin kernel serves C[M, N] = A[M, K] B[K, N].
 bool thin_eligible(int64_t M, int64_t N, int64_t K) {
     if (N > 32 || N * 8 >= M) return false;
@@ -882,6 +987,25 @@ bool thin_eligible(int64_t M, int64_t N, int64_t K) {
 template <bool SOFTMAX = false>
 int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
                 int flags) {
+    const int kv = std::max(1, (K + 255) / 256);
+    if (N <= 16) {
+        // 4 rows per group, at most one work-group per CU (each stages B)
+        const unsigned blocks = (unsigned)std::max<int64_t>(
+            1, std::min<int64_t>(((int64_t)M + 3) / 4, device_cu_count()));
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(blocks), dim3(1024), 0, stream(), A, B, C, M, N, K, bias,
+                               flags);
+            return check_launch("sgemm_thin_rows_kernel");
+        };
+        if (N <= 8) {
+            if (kv <= 1) return go(sgemm_thin_rows_kernel<8, 1, SOFTMAX>);
+            if (kv <= 2) return go(sgemm_thin_rows_kernel<8, 2, SOFTMAX>);
+            return go(sgemm_thin_rows_kernel<8, 4, SOFTMAX>);
+        }
+        if (kv <= 1) return go(sgemm_thin_rows_kernel<16, 1, SOFTMAX>);
+        if (kv <= 2) return go(sgemm_thin_rows_kernel<16, 2, SOFTMAX>);
+        return go(sgemm_thin_rows_kernel<16, 4, SOFTMAX>);
+    }
     // Enough waves to cover the rows once, at most one work-group per CU
     // (each work-group stages all of B).
     const unsigned blocks = (unsigned)std::max<int64_t>(
@@ -891,17 +1015,6 @@ int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, c
                            flags);
         return check_launch("sgemm_thin_kernel");
     };
-    const int kv = std::max(1, (K + 255) / 256);
-    if (N <= 8) {
-        if (kv <= 1) return go(sgemm_thin_kernel<8, 1, SOFTMAX>);
-        if (kv <= 2) return go(sgemm_thin_kernel<8, 2, SOFTMAX>);
-        return go(sgemm_thin_kernel<8, 4, SOFTMAX>);
-    }
-    if (N <= 16) {
-        if (kv <= 1) return go(sgemm_thin_kernel<16, 1, SOFTMAX>);
-        if (kv <= 2) return go(sgemm_thin_kernel<16, 2, SOFTMAX>);
-        return go(sgemm_thin_kernel<16, 4, SOFTMAX>);
-    }
     if (kv <= 1) return go(sgemm_thin_kernel<32, 1, SOFTMAX>);
     return go(sgemm_thin_kernel<32, 2, SOFTMAX>);
 }
