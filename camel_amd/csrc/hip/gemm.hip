@@ -4,7 +4,8 @@
 // (modules/tensor/operators.cpp:757-766) and defines conv2d / dense on the
 // same core.
 //
-// Main kernel (sgemm_kernel: one template, four operand loaders,
+// Main kernel (sgemm_kernel: one template, operand loaders for dense A/B,
+// im2col gathers from NCHW, NHWC / NCHW4 k-quads and NCHW channel planes,
 // v_mfma_f32_32x32x2_f32):
 //   * work-group tile BM x BN, K consumed in stages of BK; WM x WN waves, each
 //     owning (BM/WM) x (BN/WN) = FM x FN blocks of 32x32, optionally times WK
@@ -48,10 +49,21 @@ constexpr int GROUP_M = 4;
 // float at a time; LOAD_NHWC reads x in NHWC with K ordered (kh, kw, c), so
 // each k-quad of a pixel is one 16-byte load (needs C % BK == 0).
 // LOAD_NHWC_POOL is LOAD_NHWC with the columns in pool-window order and a
-// 2x2 max-pool epilogue (the fused conv2d..maxpool2d).
-enum { LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3, LOAD_NHWC_POOL = 4 };
+// 2x2 max-pool epilogue (the fused conv2d..maxpool2d).  LOAD_PLANES and
+// LOAD_PLANES_POOL read NCHW x in place with the same K order: a k-quad of a
+// pixel is 4 loads from 4 channel planes, and a wave's lanes take consecutive
+// pixels, so each load instruction reads a contiguous run of one plane.
+enum {
+    LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3, LOAD_NHWC_POOL = 4,
+    LOAD_PLANES = 5, LOAD_PLANES_POOL = 6
+};
 
-template <int M> constexpr bool is_nhwc = (M == LOAD_NHWC || M == LOAD_NHWC_POOL);
+// Loaders that take (pixel, k-quad) items over K ordered (kh, kw, c).
+template <int M>
+constexpr bool is_nhwc = (M == LOAD_NHWC || M == LOAD_NHWC_POOL || M == LOAD_PLANES ||
+                          M == LOAD_PLANES_POOL);
+template <int M> constexpr bool is_planes = (M == LOAD_PLANES || M == LOAD_PLANES_POOL);
+template <int M> constexpr bool is_pool = (M == LOAD_NHWC_POOL || M == LOAD_PLANES_POOL);
 template <int M> constexpr bool is_conv = (M == LOAD_CONV || is_nhwc<M>);
 
 // WK > 1 splits each stage's K range over WK groups of WM x WN waves (more
@@ -109,7 +121,20 @@ struct GemmArgs {
     // max pool over a PH x PW grid (PP = PH * PW windows per image); C is the
     // pooled output [batch][M][PP]
     int PW, PP;
+    // LOAD_PLANES: distance between channel planes (H * W); pxs = 1 and
+    // cqs = 4 * H * W
+    int chs;
 };
+
+// (pixel, k-quad) of B item q of a stage: NHWC-style loaders put a pixel's
+// k-quads on consecutive lanes (one 16-byte load each); the plane loaders put
+// consecutive pixels on consecutive lanes.
+template <class T, int BMODE> __device__ __forceinline__ int item_pixel(int q) {
+    return is_planes<BMODE> ? q % T::BN : q / T::KQ;
+}
+template <class T, int BMODE> __device__ __forceinline__ int item_kquad(int q) {
+    return is_planes<BMODE> ? q / T::BN : q % T::KQ;
+}
 
 // Value of lane Q of this lane's quad (lanes 4i .. 4i+3): a DPP quad_perm
 // move, one VALU op with no LDS traffic.
@@ -204,10 +229,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < T::BN_ITEMS; ++i) {
             const int q = tid + i * T::THREADS;
-            const int pg = n0 + q / T::KQ;
+            const int pg = n0 + item_pixel<T, BMODE>(q);
             if (pg < g.N) {
                 int img, oh, ow;
-                if constexpr (BMODE == LOAD_NHWC_POOL) {
+                if constexpr (is_pool<BMODE>) {
                     // column = ((img * PP + window) * 4 + 2 dy + dx)
                     img = pg / (4 * g.PP);
                     const int r = pg - img * 4 * g.PP, win = r >> 2, d = r & 3;
@@ -222,7 +247,8 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 }
                 px_ih[i] = oh * g.stride - g.pad;
                 px_iw[i] = ow * g.stride - g.pad;
-                px_base[i] = img * g.CHW + (px_ih[i] * g.W + px_iw[i]) * g.pxs + (q % T::KQ) * g.cqs;
+                px_base[i] = img * g.CHW + (px_ih[i] * g.W + px_iw[i]) * g.pxs +
+                             item_kquad<T, BMODE>(q) * g.cqs;
             } else {
                 px_ih[i] = -(1 << 28); // never in range
                 px_iw[i] = 0;
@@ -288,10 +314,17 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < T::BN_ITEMS; ++i) {
                 const int ih = px_ih[i] + kh, iw = px_iw[i] + kw;
-                rbn[i] = ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W &&
-                          (FULL || k0 < kend))
-                             ? *reinterpret_cast<const float4 *>(g.B + (size_t)(px_base[i] + koff))
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
+                const bool in = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W &&
+                                (FULL || k0 < kend);
+                const float *src = g.B + (size_t)(px_base[i] + koff);
+                if constexpr (is_planes<BMODE>) {
+                    rbn[i] = in ? make_float4(src[0], src[g.chs], src[2 * (size_t)g.chs],
+                                              src[3 * (size_t)g.chs])
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    rbn[i] = in ? *reinterpret_cast<const float4 *>(src)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
             }
         }
 #pragma unroll
@@ -357,7 +390,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < T::BN_ITEMS; ++i) {
                 const int q = tid + i * T::THREADS;
-                const int kq = q % T::KQ, n = q / T::KQ;
+                const int kq = item_kquad<T, BMODE>(q), n = item_pixel<T, BMODE>(q);
                 *reinterpret_cast<float4 *>(Bs + kq * T::B_PLANE + b_slot(n) * 4) = rbn[i];
             }
         }
@@ -579,7 +612,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     };
     // Tiles inside M x N (most of them) store with no row / column guards.
     const bool full_out = g.partial == nullptr && m0 + T::BM <= g.M && n0 + T::BN <= g.N;
-    if constexpr (BMODE == LOAD_NHWC_POOL) {
+    if constexpr (is_pool<BMODE>) {
         if (full_out) {
             with_flags([&](auto bias_tag, auto relu_tag) {
 #pragma unroll
@@ -1658,7 +1691,7 @@ int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char 
     CAMEL_RETURN_IF(check_launch(name));
     if (splits > 1) {
         const size_t total = (size_t)ntiles * T::BM * T::BN;
-        if (BMODE == LOAD_NHWC_POOL)
+        if (is_pool<BMODE>)
             hipLaunchKernelGGL((tile_reduce_kernel<T::BM, T::BN, true, true>),
                                dim3(grid_for((int64_t)total / 4, 256)), dim3(256), 0, stream(), g,
                                ntiles, splits);
@@ -1899,51 +1932,46 @@ GemmArgs conv_args(const float *w, const float *x, const float *bias, float *y, 
     return g;
 }
 
-// NHWC implicit GEMM: an NCHW x is transposed to NHWC (NHWC and NCHW4 are
-// read in place) and w reordered to (kh, kw, c) in pooled scratch
-// (stream-ordered, returned to the pool after the launch).  pool: y is the
-// 2x2 stride-2 max pool of the convolution, [N][Co][OH/2][OW/2], written from
-// the GEMM epilogue.
+// Implicit GEMM over K ordered (kh, kw, c), x read in place: NHWC and NCHW4
+// with one 16-byte load per k-quad of a pixel, NCHW with one load per channel
+// plane (LOAD_PLANES; against transposing x to NHWC first, which moved 2 x
+// 51 MB more per call: config-4 conv 291 -> 287 us, the CNN's conv2 from
+// NCHW 160 -> 154 us).  w is reordered to (kh, kw, c) in pooled scratch
+// (stream-ordered, returned to the pool after the launch) unless it comes
+// packed.  pool: y is the 2x2 stride-2 max pool of the convolution,
+// [N][Co][OH/2][OW/2], written from the GEMM epilogue.
 template <class T>
 int conv2d_nhwc(const float *x, const float *w, const float *bias, float *y, int64_t N, int64_t C,
                 int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
                 int64_t pad, int64_t OH, int64_t OW, int flags, Layout x_layout, bool pool,
                 bool w_packed) {
-    const bool in_place = x_layout != L_NCHW;
+    const bool planes = x_layout == L_NCHW;
     const int64_t HW = H * W, K = C * KH * KW;
-    Scratch xt, wt;
-    // packed weights (already (kh, kw, c)): nothing to reorder; the
-    // transpose's weight slice is then given none
-    const int64_t co_reorder = w_packed ? 0 : Co;
-    if (!w_packed) CAMEL_RETURN_IF(wt.alloc((size_t)(Co * K) * sizeof(float)));
-    const float *wk = w_packed ? w : wt.f();
-    if (!in_place) {
-        CAMEL_RETURN_IF(xt.alloc((size_t)(N * C * HW) * sizeof(float)));
-        // xt comes from the pool (256-byte aligned); x is 16-byte aligned here.
-        const bool vec = HW % 4 == 0 && C % 4 == 0;
-        const int tp = vec ? TP_VEC : 32;
-        dim3 tgrid((unsigned)((HW + tp - 1) / tp), (unsigned)((C + 31) / 32), (unsigned)(N + 1));
-        if (vec)
-            hipLaunchKernelGGL(nchw_to_nhwc_kernel<true>, tgrid, dim3(256), 0, stream(), x, xt.f(),
-                               (int)C, (int)HW, w, wt.f(), (int)co_reorder, (int)(KH * KW));
-        else
-            hipLaunchKernelGGL(nchw_to_nhwc_kernel<false>, tgrid, dim3(256), 0, stream(), x, xt.f(),
-                               (int)C, (int)HW, w, wt.f(), (int)co_reorder, (int)(KH * KW));
-        CAMEL_RETURN_IF(check_launch("nchw_to_nhwc_kernel"));
-    } else if (!w_packed) {
+    Scratch wt;
+    if (!w_packed) {
+        CAMEL_RETURN_IF(wt.alloc((size_t)(Co * K) * sizeof(float)));
         CAMEL_RETURN_IF(pack_weights(w, wt.f(), Co, C, KH * KW));
     }
-    GemmArgs g = conv_args(wk, in_place ? x : xt.f(), bias, y, N, C, H, W, Co, KH, KW, stride, pad,
+    GemmArgs g = conv_args(w_packed ? w : wt.f(), x, bias, y, N, C, H, W, Co, KH, KW, stride, pad,
                            OH, OW, flags);
     if (x_layout == L_NCHW4) {
         g.pxs = 4;
         g.cqs = (int)(4 * HW);
+    } else if (planes) {
+        g.pxs = 1;
+        g.cqs = (int)(4 * HW);
+        g.chs = (int)HW;
     }
     if (pool) {
         g.PW = (int)(OW / 2);
         g.PP = (int)((OH / 2) * (OW / 2));
         g.N = (int)(N * g.PP * 4);
-        CAMEL_RETURN_IF((run_gemm<T, LOAD_VEC, LOAD_NHWC_POOL>(g, 1, "conv2d_pool_kernel")));
+        if (planes)
+            CAMEL_RETURN_IF((run_gemm<T, LOAD_VEC, LOAD_PLANES_POOL>(g, 1, "conv2d_pool_kernel")));
+        else
+            CAMEL_RETURN_IF((run_gemm<T, LOAD_VEC, LOAD_NHWC_POOL>(g, 1, "conv2d_pool_kernel")));
+    } else if (planes) {
+        CAMEL_RETURN_IF((run_gemm<T, LOAD_VEC, LOAD_PLANES>(g, 1, "conv2d_planes_kernel")));
     } else {
         CAMEL_RETURN_IF((run_gemm<T, LOAD_VEC, LOAD_NHWC>(g, 1, "conv2d_nhwc_kernel")));
     }
