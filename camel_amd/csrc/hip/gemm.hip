@@ -196,7 +196,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     block_pos(local, split);
     tile_of(g.tile_begin + local, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * T::BM, n0 = g.n_begin + tn * T::BN;
-    const int kbeg = split * g.k_per_split;
+    // K is consumed in whole stages: when BK does not divide K, the ragged
+    // part is the first stage of split 0, which starts kpad below k = 0 and
+    // is loaded with guards (zeros below 0); every later stage is a whole BK
+    // and the loop body keeps guard-free loads.  (The conv loaders have
+    // K % BK == 0.)
+    const int kpad = is_nhwc<BMODE> ? 0 : (T::BK - g.K % T::BK) % T::BK;
+    const int kbeg = split * g.k_per_split - kpad;
     const int kend = min(g.K, kbeg + g.k_per_split);
     const int nk = kend > kbeg ? (kend - kbeg + T::BK - 1) / T::BK : 0;
 
@@ -281,8 +287,9 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         }
     }
 
-    // FULL: the tile lies inside M x N and every stage is a whole BK of K, so
-    // the row/column/k guards compile away (interior tiles of most problems).
+    // FULL: the tile lies inside M x N and the stage is a whole BK inside
+    // [0, K), so the row/column/k guards compile away (every stage of the
+    // interior tiles but a ragged first one).
     auto load_stage = [&](auto full_tag, int k0, StageRegs &R) {
         constexpr bool FULL = decltype(full_tag)::value;
         float4 *ra = R.ra;
@@ -296,14 +303,15 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             const int gm = m0 + m, gk = k0 + 4 * kq;
             const float *src = g.A + (size_t)gm * g.lda + gk;
             if constexpr (AMODE == LOAD_VEC) {
-                ra[i] = (FULL || (gm < g.M && gk < kend)) ? *reinterpret_cast<const float4 *>(src)
+                ra[i] = (FULL || (gm < g.M && gk >= 0 && gk < kend))
+                            ? *reinterpret_cast<const float4 *>(src)
                                                           : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
                 const bool rv = FULL || gm < g.M;
-                ra[i].x = (rv && (FULL || gk + 0 < kend)) ? src[0] : 0.f;
-                ra[i].y = (rv && (FULL || gk + 1 < kend)) ? src[1] : 0.f;
-                ra[i].z = (rv && (FULL || gk + 2 < kend)) ? src[2] : 0.f;
-                ra[i].w = (rv && (FULL || gk + 3 < kend)) ? src[3] : 0.f;
+                ra[i].x = (rv && (FULL || (gk + 0 >= 0 && gk + 0 < kend))) ? src[0] : 0.f;
+                ra[i].y = (rv && (FULL || (gk + 1 >= 0 && gk + 1 < kend))) ? src[1] : 0.f;
+                ra[i].z = (rv && (FULL || (gk + 2 >= 0 && gk + 2 < kend))) ? src[2] : 0.f;
+                ra[i].w = (rv && (FULL || (gk + 3 >= 0 && gk + 3 < kend))) ? src[3] : 0.f;
             }
         }
         if constexpr (is_nhwc<BMODE>) {
@@ -337,7 +345,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
-                    rb[i][u] = (FULL || (gn < g.N && gk < kend))
+                    rb[i][u] = (FULL || (gn < g.N && gk >= 0 && gk < kend))
                                    ? *reinterpret_cast<const float4 *>(g.B + (size_t)gk * g.ldb + gn)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
@@ -350,7 +358,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         const int gn = n0 + nq + c * (T::BN / 4);
-                        v[c] = (FULL || (gn < g.N && gk < kend)) ? row[gn] : 0.f;
+                        v[c] = (FULL || (gn < g.N && gk >= 0 && gk < kend)) ? row[gn] : 0.f;
                     }
                     rb[i][u] = make_float4(v[0], v[1], v[2], v[3]);
                 }
@@ -359,7 +367,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
                     float v[4] = {0.f, 0.f, 0.f, 0.f};
-                    if (FULL || gk < kend) {
+                    if (FULL || (gk >= 0 && gk < kend)) {
                         const int2 e = g.ktab[gk];
                         const int kh = e.y >> 16, kw = e.y & 0xffff;
 #pragma unroll
@@ -473,7 +481,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 
     auto main_loop = [&](auto full_tag) {
         if (nk <= 0) return;
-        load_stage(full_tag, kbeg, R0);
+        if (kbeg < 0)
+            load_stage(std::false_type{}, kbeg, R0); // the ragged first stage
+        else
+            load_stage(full_tag, kbeg, R0);
         store_stage(smem, smem + T::A_STAGE, R0);
         __syncthreads();
         float4 fa[2][T::FM], fb[2][T::FN];
@@ -525,8 +536,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
         }
     };
-    const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N) &&
-                           (kend - kbeg) % T::BK == 0;
+    const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N);
     if (full_tile)
         main_loop(std::true_type{});
     else
