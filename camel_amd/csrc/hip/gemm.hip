@@ -1591,6 +1591,7 @@ __global__ __launch_bounds__(PIXB) void conv2d_direct_nhwc_kernel(
 using TileBig = Tile<256, 256, 32, 2, 4, 1, false>; // wave 128x64, 8 waves
 using TileMid = Tile<128, 128, 32, 2, 2>;           // wave 64x64
 using TileSmall = Tile<64, 64, 64, 2, 2, 2>;        // wave 32x32, two k-groups (8 waves)
+using TileTiny = Tile<32, 32, 64, 1, 1, 4>;         // one 32x32 block, four k-groups (4 waves)
 using TileSkinny = Tile<32, 128, 64, 1, 4>;  // M <= 32 when the streaming kernel cannot run
 using TileConv = Tile<128, 128, 32, 2, 2>;   // NHWC conv, Co > 64, C % 32 == 0
 using TileConv16 = Tile<128, 128, 16, 2, 2>; // NHWC conv, Co > 64, C % 16 == 0
@@ -1764,7 +1765,7 @@ template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool
     return run_gemm<T, LOAD_SCALAR, LOAD_SCALAR>(g, splits, "sgemm_kernel");
 }
 
-enum class Cfg { Big, Mid, Small, Skinny };
+enum class Cfg { Big, Mid, Small, Tiny, Skinny };
 
 // Picks a tile shape and split count so the grid covers the chip's CUs.
 void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int &bk) {
@@ -1789,9 +1790,22 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
         if (tiles >= cus) return;
     }
     // Split K so tiles*splits fills the chip, keeping >= 4 stages per split.
-    const int64_t want = (cus + tiles - 1) / tiles;
-    const int64_t max_splits = std::max<int64_t>(1, K / (4 * bk));
-    splits = (int)std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(max_splits, 64)));
+    auto split_for = [&](int64_t t) {
+        const int64_t want = (cus + t - 1) / t;
+        const int64_t max_splits = std::max<int64_t>(1, K / (4 * bk));
+        return (int)std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(max_splits, 64)));
+    };
+    splits = split_for(tiles);
+    // A short K leaves too few 64 x 64 work-groups to cover half the CUs
+    // (e.g. the 256^3 matmul: 16): 32 x 32 tiles, four times as many
+    // (256^3: 7.5 -> 5.0 us).  Not when splits already fill the chip (the
+    // CNN's 512x9216 -> 128 layer measured 21 us with 64 x 64 x 16 splits
+    // against 30 us with 32 x 32 x 4).
+    if (cfg == Cfg::Small && tiles * splits * 2 < cus) {
+        cfg = Cfg::Tiny;
+        tiles = tiles_of<TileTiny>(M, N);
+        splits = split_for(tiles);
+    }
 }
 
 // ---- conv2d host paths -----------------------------------------------------------
@@ -2213,6 +2227,9 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
         break;
     case Cfg::Mid:
         rc = launch_gemm_modes<TileMid>(g, splits, avec, bvec);
+        break;
+    case Cfg::Tiny:
+        rc = launch_gemm_modes<TileTiny>(g, splits, avec, bvec);
         break;
     case Cfg::Small:
         rc = launch_gemm_modes<TileSmall>(g, splits, avec, bvec);
