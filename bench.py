@@ -397,6 +397,11 @@ def main() -> int:
             suite[f"sgemm_{n}"] = {"value": round(r["value"], 1), "unit": "GFLOP/s",
                                    "ms": round(r["ms"], 4),
                                    "roofline": roofline_mfma(r["flop"], r["ms"])}
+        r = wl_gemm(256, 256, 256, s_steps, s_warm)
+        suite["matmul_256"] = {"value": round(r["value"], 1), "unit": "GFLOP/s",
+                               "ms": round(r["ms"], 4),
+                               "note": "BASELINE config 1 (plumbing anchor): launch-latency bound",
+                               "roofline": roofline_mfma(r["flop"], r["ms"])}
         r = wl_gemm_host(4096, 5, 2)
         suite["sgemm_4096_host_operands"] = {
             "value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1), "unit": "GFLOP/s",
