@@ -41,6 +41,27 @@ def test_sgemm_matches_oracle(M, N, Kd):
     assert ok, f"worst error / bound = {worst}"
 
 
+@pytest.mark.parametrize("M,N,Kd", [
+    (512, 256, 2000),    # 64x64 tiles, 7 K splits, K % 64 = 16
+    (1024, 2048, 1000),  # 64x64 tiles, no split, K % 64 = 40
+    (2048, 2048, 1001),  # 128x128 tiles, odd K (scalar A loads), K % 32 = 9
+    (4096, 4096, 1000),  # 256x256 tiles, K % 32 = 8
+    (200, 72, 1000),     # 32x32 tiles, K splits, K % 64 = 40
+])
+def test_ragged_k_first_stage(M, N, Kd):
+    # When BK does not divide K the first stage of split 0 starts below k = 0
+    # and is loaded with guards; every later stage is whole.  Rows from the
+    # first, a middle and the last tile row, against the oracle's fp64 k-order
+    # loop.
+    a, b = _ab(M, N, Kd, 0x1500 + M + N + Kd)
+    bias = D.uniform(0x1600 + N, (N,), -1.0, 1.0)
+    got = K.sgemm(a, b, bias, H.EPI_BIAS)
+    for r0, r1 in ((0, 8), (M // 2 - 3, M // 2 + 3), (M - 8, M)):
+        ref = O.dense(a[r0:r1], b, bias, False)
+        ok, worst = K.gemm_tol_ok(got[r0:r1], ref, a[r0:r1], b)
+        assert ok, f"rows {r0}-{r1}: worst error / bound = {worst}"
+
+
 def test_sgemm_zero_k_gives_zeros():
     a = np.zeros((5, 0), np.float32)
     b = np.zeros((0, 7), np.float32)
