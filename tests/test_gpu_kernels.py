@@ -295,10 +295,10 @@ def test_conv2d_matches_oracle(N, Cin, H_, W_, Co, k, stride, pad):
 
 
 @pytest.mark.parametrize("N,Cin,H_,W_,Co,kh,kw,stride,pad", [
-    (2, 64, 17, 15, 96, 3, 3, 2, 1),    # NHWC path, 128-row tile, stride 2, ragged tiles
-    (3, 32, 12, 10, 40, 3, 5, 1, 2),    # NHWC path, 64-row tile, KH != KW, wide pad
-    (1, 64, 9, 9, 200, 1, 1, 1, 0),     # NHWC path, 1x1 kernel, two row tiles
-    (2, 48, 7, 7, 150, 3, 3, 1, 1),     # NHWC path with C = 48 (3 stages per (kh, kw))
+    (2, 64, 17, 15, 96, 3, 3, 2, 1),    # implicit GEMM (channel-plane loads), 128-row tile, stride 2
+    (3, 32, 12, 10, 40, 3, 5, 1, 2),    # implicit GEMM, 64-row tile, KH != KW, wide pad
+    (1, 64, 9, 9, 200, 1, 1, 1, 0),     # implicit GEMM, 1x1 kernel, two row tiles
+    (2, 48, 7, 7, 150, 3, 3, 1, 1),     # implicit GEMM with C = 48 (3 stages per (kh, kw))
     (2, 12, 8, 8, 24, 3, 3, 1, 1),      # gather path: C % 16 != 0, K = 108
     (4, 2, 10, 10, 33, 4, 4, 2, 1),     # direct path, K = 32, Co not a multiple of 8
     (2, 3, 16, 16, 16, 3, 3, 1, 1),     # direct, K = 27, 2 pixels per thread
