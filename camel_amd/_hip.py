@@ -66,6 +66,7 @@ _SIGNATURES = {
     "camel_hip_conv2d_pool2": [_P, _P, _P, _P] + [_I64] * 9 + [_I],
     "camel_hip_conv2d_pack_weights": [_P, _P] + [_I64] * 4,
     "camel_hip_dense_softmax": [_P, _P, _P, _P, _I64, _I64, _I64, _I],
+    "camel_hip_dense_head": [_P, _P, _P, _P, _P, _P] + [_I64] * 4 + [_I, _I, _I],
     "camel_hip_maxpool2d": [_P, _P] + [_I64] * 7,
     "camel_hip_binary": [_I, _I, _P, _I, _P, _I, _P, _I64],
     "camel_hip_binary_scalar": [_I, _I, _I, _P, _D, _I, _P, _I64],

@@ -169,6 +169,13 @@ __device__ __forceinline__ void tile_of(int id, int tiles_m, int tiles_n, int &t
     tn = in_group / gsize;
 }
 
+// Inverse of tile_of: the logical tile id of tile (tm, tn).
+__device__ __forceinline__ int tile_id(int tm, int tn, int tiles_m, int tiles_n) {
+    const int g = tm / GROUP_M, first_m = g * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    return g * GROUP_M * tiles_n + tn * gsize + (tm - first_m);
+}
+
 // Position of this work-group: its tile (local to the launch, which covers
 // tiles [tile_begin, tile_begin + gridDim.x)) and its K split (gridDim.y
 // splits).  Work-groups are dispatched round-robin over the 8 XCDs in linear
@@ -778,6 +785,23 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 // stores with the GEMM (row-major) or conv (NCHW or NCHW4) output mapping.
 // POOL (pooled conv): one thread per pool window (4 consecutive columns of
 // a tile), max of the 4 finished values in window order.
+// sum_z partial[z * total + idx] for z = 0 .. splits-1, added in split order;
+// loads go out 8 at a time so their latencies overlap.
+__device__ __forceinline__ float sum_splits(const float *__restrict__ partial, size_t total,
+                                            size_t idx, int splits) {
+    float s = partial[idx];
+    int z = 1;
+    for (; z + 8 <= splits; z += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = partial[(size_t)(z + u) * total + idx];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s = s + t[u];
+    }
+    for (; z < splits; ++z) s = s + partial[(size_t)z * total + idx];
+    return s;
+}
+
 template <int BM, int BN, bool CONV, bool POOL = false>
 __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles, int splits) {
     const int tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N - g.n_begin + BN - 1) / BN;
@@ -795,8 +819,7 @@ __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles
             float mx = 0.f;
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                float s = g.partial[idx + d];
-                for (int z = 1; z < splits; ++z) s = s + g.partial[(size_t)z * total + idx + d];
+                float s = sum_splits(g.partial, total, idx + d, splits);
                 if (g.flags & CAMEL_EPI_BIAS) s = s + g.bias[row];
                 if (g.flags & CAMEL_EPI_RELU) s = relu_idiom(s);
                 if (d == 0 || s > mx) mx = s;
@@ -815,8 +838,7 @@ __global__ __launch_bounds__(256) void tile_reduce_kernel(GemmArgs g, int ntiles
         tile_of(g.tile_begin + local, tiles_m, tiles_n, tm, tn);
         const int row = tm * BM + w / BN, col = g.n_begin + tn * BN + w % BN;
         if (row >= g.M || col >= g.N) continue;
-        float s = g.partial[idx];
-        for (int z = 1; z < splits; ++z) s = s + g.partial[(size_t)z * total + idx];
+        float s = sum_splits(g.partial, total, idx, splits);
         if (g.flags & CAMEL_EPI_BIAS) s = s + (CONV ? g.bias[row] : g.bias[col]);
         if (g.flags & CAMEL_EPI_RELU) s = relu_idiom(s);
         if constexpr (CONV) {
@@ -925,8 +947,35 @@ __global__ __launch_bounds__(256) void sgemm_thin_kernel(const float *__restrict
     }
 }
 
-template <int NT, int KV, bool SOFTMAX = false>
-__global__ __launch_bounds__(1024) void sgemm_thin_rows_kernel(const float *__restrict__ A,
+// Row sources of the thin kernel's A operand: A[m][k] of a row-major matrix,
+// or of the result of a split-K GEMM still in its partials, rebuilt the way
+// tile_reduce_kernel finishes it (the splits added in split order, then the
+// column bias and relu of that GEMM's epilogue), so a dense layer can feed
+// the thin kernel without its reduce launch and with the same values.
+struct RowsA {
+    const float *A;
+    int K;
+    __device__ __forceinline__ float operator()(int m, int k) const { return A[(size_t)m * K + k]; }
+};
+struct SplitPartialsA {
+    const float *partial; // [split][tile][BM * BN], tiles in tile_of order
+    const float *bias;    // column bias of the GEMM (CAMEL_EPI_BIAS), or null
+    int flags;            // that GEMM's epilogue flags
+    int splits, ntiles, tiles_m, tiles_n, BM, BN;
+    __device__ __forceinline__ float operator()(int m, int k) const {
+        const int tm = m / BM, tn = k / BN;
+        const size_t total = (size_t)ntiles * BM * BN;
+        const size_t idx = (size_t)tile_id(tm, tn, tiles_m, tiles_n) * BM * BN +
+                           (size_t)(m - tm * BM) * BN + (k - tn * BN);
+        float v = sum_splits(partial, total, idx, splits);
+        if (flags & CAMEL_EPI_BIAS) v = v + bias[k];
+        if (flags & CAMEL_EPI_RELU) v = relu_idiom(v);
+        return v;
+    }
+};
+
+template <int NT, int KV, bool SOFTMAX = false, class ASrc = RowsA>
+__global__ __launch_bounds__(1024) void sgemm_thin_rows_kernel(const ASrc src,
                                                                const float *__restrict__ B,
                                                                float *__restrict__ C, int M, int N,
                                                                int K, const float *__restrict__ bias,
@@ -945,7 +994,7 @@ __global__ __launch_bounds__(1024) void sgemm_thin_rows_kernel(const float *__re
 #pragma unroll
         for (int i = 0; i < KV; ++i) {
             const int k = q * KQ + lane + 64 * i;
-            av[i] = (m < M && k < K) ? A[(size_t)m * K + k] : 0.f;
+            av[i] = (m < M && k < K) ? src(m, k) : 0.f;
         }
     };
     int grp = blockIdx.x;
@@ -1027,28 +1076,34 @@ bool thin_eligible(int64_t M, int64_t N, int64_t K) {
     return K <= (N <= 16 ? 1024 : 512);
 }
 
+// N <= 16 (and K <= 1024): the 16-wave kernel over rows from `src`.
+template <bool SOFTMAX, class ASrc>
+int launch_thin_rows(const ASrc &src, const float *B, float *C, int M, int N, int K,
+                     const float *bias, int flags) {
+    const int kv = std::max(1, (K + 255) / 256);
+    // 4 rows per group, at most one work-group per CU (each stages B)
+    const unsigned blocks = (unsigned)std::max<int64_t>(
+        1, std::min<int64_t>(((int64_t)M + 3) / 4, device_cu_count()));
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(blocks), dim3(1024), 0, stream(), src, B, C, M, N, K, bias,
+                           flags);
+        return check_launch("sgemm_thin_rows_kernel");
+    };
+    if (N <= 8) {
+        if (kv <= 1) return go(sgemm_thin_rows_kernel<8, 1, SOFTMAX, ASrc>);
+        if (kv <= 2) return go(sgemm_thin_rows_kernel<8, 2, SOFTMAX, ASrc>);
+        return go(sgemm_thin_rows_kernel<8, 4, SOFTMAX, ASrc>);
+    }
+    if (kv <= 1) return go(sgemm_thin_rows_kernel<16, 1, SOFTMAX, ASrc>);
+    if (kv <= 2) return go(sgemm_thin_rows_kernel<16, 2, SOFTMAX, ASrc>);
+    return go(sgemm_thin_rows_kernel<16, 4, SOFTMAX, ASrc>);
+}
+
 template <bool SOFTMAX = false>
 int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
                 int flags) {
     const int kv = std::max(1, (K + 255) / 256);
-    if (N <= 16) {
-        // 4 rows per group, at most one work-group per CU (each stages B)
-        const unsigned blocks = (unsigned)std::max<int64_t>(
-            1, std::min<int64_t>(((int64_t)M + 3) / 4, device_cu_count()));
-        auto go = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, dim3(blocks), dim3(1024), 0, stream(), A, B, C, M, N, K, bias,
-                               flags);
-            return check_launch("sgemm_thin_rows_kernel");
-        };
-        if (N <= 8) {
-            if (kv <= 1) return go(sgemm_thin_rows_kernel<8, 1, SOFTMAX>);
-            if (kv <= 2) return go(sgemm_thin_rows_kernel<8, 2, SOFTMAX>);
-            return go(sgemm_thin_rows_kernel<8, 4, SOFTMAX>);
-        }
-        if (kv <= 1) return go(sgemm_thin_rows_kernel<16, 1, SOFTMAX>);
-        if (kv <= 2) return go(sgemm_thin_rows_kernel<16, 2, SOFTMAX>);
-        return go(sgemm_thin_rows_kernel<16, 4, SOFTMAX>);
-    }
+    if (N <= 16) return launch_thin_rows<SOFTMAX>(RowsA{A, K}, B, C, M, N, K, bias, flags);
     // Enough waves to cover the rows once, at most one work-group per CU
     // (each work-group stages all of B).
     const unsigned blocks = (unsigned)std::max<int64_t>(
@@ -1682,9 +1737,12 @@ template <class T, int AMODE, int BMODE> int resident_slots() {
 }
 
 // Runs tiles [tile_begin, tile_begin + ntiles) with `splits` K splits; split
-// launches write partials that tile_reduce_kernel folds into C.
+// launches write partials that tile_reduce_kernel folds into C.  With
+// `partials_only` the reduce is left to the caller: the partials stay in
+// g_partial and *partials_only receives the split count they hold.
 template <class T, int AMODE, int BMODE>
-int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char *name) {
+int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char *name,
+                 int *partials_only = nullptr) {
     g.tile_begin = tile_begin;
     const int stages = (g.K + T::BK - 1) / T::BK;
     splits = std::max(1, std::min(splits, stages));
@@ -1700,6 +1758,10 @@ int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char 
     hipLaunchKernelGGL((sgemm_kernel<T, AMODE, BMODE>), dim3((unsigned)ntiles, (unsigned)splits),
                        dim3(T::THREADS), 0, stream(), g);
     CAMEL_RETURN_IF(check_launch(name));
+    if (partials_only) {
+        *partials_only = splits;
+        return CAMEL_HIP_OK;
+    }
     if (splits > 1) {
         const size_t total = (size_t)ntiles * T::BM * T::BN;
         if (is_pool<BMODE>)
@@ -1763,6 +1825,34 @@ template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool
     if (avec) return run_gemm<T, LOAD_VEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
     if (bvec) return run_gemm<T, LOAD_SCALAR, LOAD_VEC>(g, splits, "sgemm_kernel");
     return run_gemm<T, LOAD_SCALAR, LOAD_SCALAR>(g, splits, "sgemm_kernel");
+}
+
+// The split-K launch run_gemm makes for `splits` > 1, without its reduce:
+// the partials of all tiles stay in g_partial for a consumer that finishes
+// them (SplitPartialsA).  Fills the geometry that consumer needs.
+template <class T>
+int launch_split_partials(GemmArgs g, int splits, bool avec, bool bvec, SplitPartialsA &out) {
+    const int tiles_m = (g.M + T::BM - 1) / T::BM, tiles_n = (g.N + T::BN - 1) / T::BN;
+    const int tiles = tiles_m * tiles_n;
+    int used = 0;
+    if (avec && bvec)
+        CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_VEC>(g, 0, tiles, splits, "sgemm_kernel", &used)));
+    else if (avec)
+        CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_SCALAR>(g, 0, tiles, splits, "sgemm_kernel", &used)));
+    else if (bvec)
+        CAMEL_RETURN_IF((launch_range<T, LOAD_SCALAR, LOAD_VEC>(g, 0, tiles, splits, "sgemm_kernel", &used)));
+    else
+        CAMEL_RETURN_IF((launch_range<T, LOAD_SCALAR, LOAD_SCALAR>(g, 0, tiles, splits, "sgemm_kernel", &used)));
+    out.partial = g_partial;
+    out.bias = g.bias;
+    out.flags = g.flags;
+    out.splits = used;
+    out.ntiles = tiles;
+    out.tiles_m = tiles_m;
+    out.tiles_n = tiles_n;
+    out.BM = T::BM;
+    out.BN = T::BN;
+    return CAMEL_HIP_OK;
 }
 
 enum class Cfg { Big, Mid, Small, Tiny, Skinny };
@@ -2258,6 +2348,72 @@ int camel_hip_dense_softmax(const float *A, const float *B, const float *bias, f
     // (each row is read whole before it is written).
     CAMEL_RETURN_IF(camel_hip_sgemm(A, B, C, M, N, K, bias, flags));
     CAMEL_RETURN_IF(camel_hip_softmax_rows(C, C, M, N));
+    return ok();
+}
+
+int camel_hip_dense_head(const float *x, const float *w1, const float *b1, const float *w2,
+                         const float *b2, float *y, int64_t M, int64_t K1, int64_t N1, int64_t N2,
+                         int flags1, int flags2, int softmax) {
+    if (M < 0 || K1 < 0 || N1 < 0 || N2 < 0)
+        return fail(CAMEL_HIP_ERR_SHAPE, "dense_head: negative dimension");
+    if (M > INT32_MAX / 2 || K1 > INT32_MAX / 2 || N1 > INT32_MAX / 2 || N2 > INT32_MAX / 2)
+        return fail(CAMEL_HIP_ERR_SHAPE, "dense_head: dimension too large");
+    if (((flags1 & CAMEL_EPI_BIAS) && !b1) || ((flags2 & CAMEL_EPI_BIAS) && !b2))
+        return fail(CAMEL_HIP_ERR_ARG, "dense_head: null bias");
+    if ((flags1 | flags2) & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU))
+        return fail(CAMEL_HIP_ERR_ARG, "dense_head: unknown flags");
+    if (M == 0 || N2 == 0) return ok();
+    if (!y || (K1 > 0 && (!x || !w1)) || (N1 > 0 && !w2))
+        return fail(CAMEL_HIP_ERR_ARG, "dense_head: null operand");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    // Fused when layer 1 runs as a split-K GEMM of the main kernel and layer
+    // 2 as the 16-wave thin kernel: the thin kernel rebuilds layer 1's rows
+    // from the partials (no reduce launch, no intermediate in HBM).
+    Cfg cfg = Cfg::Skinny;
+    int splits = 1, bk = 0;
+    if (N2 <= 16 && thin_eligible(M, N2, N1) && !thin_eligible(M, N1, K1) && M > 32)
+        choose(M, N1, K1, device_cu_count(), cfg, splits, bk);
+    if (cfg == Cfg::Skinny || splits <= 1) {
+        Scratch h;
+        CAMEL_RETURN_IF(h.alloc((size_t)(M * N1) * sizeof(float)));
+        CAMEL_RETURN_IF(camel_hip_sgemm(x, w1, h.f(), M, N1, K1, b1, flags1));
+        if (softmax) return camel_hip_dense_softmax(h.f(), w2, b2, y, M, N2, N1, flags2);
+        return camel_hip_sgemm(h.f(), w2, y, M, N2, N1, b2, flags2);
+    }
+    GemmArgs g{};
+    g.A = x;
+    g.B = w1;
+    g.C = y; // not written: the launch leaves partials
+    g.bias = b1;
+    g.M = (int)M;
+    g.N = (int)N1;
+    g.K = (int)K1;
+    g.lda = (int)K1;
+    g.ldb = (int)N1;
+    g.ldc = (int)N1;
+    g.flags = flags1;
+    const bool avec = (K1 % 4 == 0) && ((uintptr_t)x % 16 == 0);
+    const bool bvec = (N1 % 4 == 0) && ((uintptr_t)w1 % 16 == 0);
+    SplitPartialsA src{};
+    switch (cfg) {
+    case Cfg::Big:
+        CAMEL_RETURN_IF(launch_split_partials<TileBig>(g, splits, avec, bvec, src));
+        break;
+    case Cfg::Mid:
+        CAMEL_RETURN_IF(launch_split_partials<TileMid>(g, splits, avec, bvec, src));
+        break;
+    case Cfg::Tiny:
+        CAMEL_RETURN_IF(launch_split_partials<TileTiny>(g, splits, avec, bvec, src));
+        break;
+    default:
+        CAMEL_RETURN_IF(launch_split_partials<TileSmall>(g, splits, avec, bvec, src));
+        break;
+    }
+    if (softmax)
+        CAMEL_RETURN_IF((launch_thin_rows<true>(src, w2, y, (int)M, (int)N2, (int)N1, b2, flags2)));
+    else
+        CAMEL_RETURN_IF((launch_thin_rows<false>(src, w2, y, (int)M, (int)N2, (int)N1, b2, flags2)));
     return ok();
 }
 

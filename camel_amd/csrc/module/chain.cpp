@@ -161,6 +161,21 @@ std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> sha
             if (j < n && steps_[j].kind == LayerKind::Softmax) {
                 g.kind = Group::DenseSoftmax;
                 ++j;
+            } else if (j < n && steps_[j].kind == LayerKind::Dense && steps_[j].w->rank() == 2 &&
+                       steps_[j].w->dim(1) <= 16) {
+                // a narrow second dense: the pair runs as one head
+                g.kind = Group::DenseHead;
+                g.step2 = &steps_[j];
+                g.relu2 = steps_[j].relu;
+                ++j;
+                if (!g.relu2 && j < n && steps_[j].kind == LayerKind::Relu) {
+                    g.relu2 = true;
+                    ++j;
+                }
+                if (j < n && steps_[j].kind == LayerKind::Softmax) {
+                    g.softmax = true;
+                    ++j;
+                }
             }
             batch = -1;
             break;
@@ -214,6 +229,10 @@ std::string LayerChain::plan(std::span<const int64_t> shape) const {
         case Group::DenseSoftmax:
             out << (g.relu ? "dense_relu+softmax" : "dense+softmax");
             break;
+        case Group::DenseHead:
+            out << (g.relu ? "dense_relu+" : "dense+") << (g.relu2 ? "dense_relu" : "dense");
+            if (g.softmax) out << "+softmax";
+            break;
         case Group::Conv:
             out << (g.relu ? "conv2d_relu" : "conv2d");
             if (g.pool) out << "+maxpool2d(2,2)";
@@ -257,6 +276,10 @@ TensorObject *LayerChain::apply(const TensorObject *x) const {
             break;
         case Group::DenseSoftmax:
             next = Activation::of(tensorDenseSoftmax(cur.tensor, s.w, s.bias, g.relu));
+            break;
+        case Group::DenseHead:
+            next = Activation::of(tensorDenseHead(cur.tensor, s.w, s.bias, g.relu, g.step2->w,
+                                                  g.step2->bias, g.relu2, g.softmax));
             break;
         case Group::Relu:
             next = Activation::of(tensorRelu(cur.tensor));

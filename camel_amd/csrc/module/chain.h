@@ -8,6 +8,10 @@
 //   dense + relu, conv2d + relu       -> the GEMM epilogue (as dense_relu,
 //                                        conv2d_relu)
 //   dense (+relu) + softmax           -> camel_hip_dense_softmax
+//   dense (+relu) + dense with N <= 16 (+relu) (+softmax)
+//                                     -> camel_hip_dense_head (the second
+//                                        layer's kernel adds the first
+//                                        one's split-K partials)
 //   conv2d (+relu) + maxpool2d(2, 2)  -> camel_hip_conv2d_pool2
 //   conv2d -> conv2d that reads NCHW4 -> the first writes NCHW4
 //                                        ([N][C/4][H][W][4]) and the second
@@ -66,9 +70,12 @@ public:
 
 private:
     struct Group {
-        enum Kind { Dense, DenseSoftmax, Conv, Relu, Softmax, MaxPool, Reshape } kind;
+        enum Kind { Dense, DenseSoftmax, DenseHead, Conv, Relu, Softmax, MaxPool, Reshape } kind;
         const LayerStep *step; // first layer of the group
+        const LayerStep *step2 = nullptr; // DenseHead: the second dense
         bool relu = false;
+        bool relu2 = false;    // DenseHead: relu after the second dense
+        bool softmax = false;  // DenseHead: row softmax at the end
         bool pool = false;     // conv + maxpool2d(2, 2)
         bool x_nchw4 = false;  // conv input comes NCHW4 from the previous conv
         bool y_nchw4 = false;  // conv output goes NCHW4 to the next conv

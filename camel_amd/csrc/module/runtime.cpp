@@ -483,6 +483,58 @@ TensorObject *tensorDenseSoftmax(const TensorObject *x, const TensorObject *w,
     return out;
 }
 
+// dense (relu) then dense (relu) (then softmax): a classifier head of
+// README.md:40-46.  Float32 runs camel_hip_dense_head (layer 2's kernel adds
+// layer 1's split-K partials itself where layer 1 splits K; the values of
+// the two layers' functions either way); other dtypes and empty inner
+// dimensions run tensorDense then tensorDense / tensorDenseSoftmax.
+TensorObject *tensorDenseHead(const TensorObject *x, const TensorObject *w1,
+                              const TensorObject *b1, bool relu1, const TensorObject *w2,
+                              const TensorObject *b2, bool relu2, bool softmax) {
+    auto check = [](const TensorObject *a, const TensorObject *w, const TensorObject *b) {
+        if (a->rank() != 2 || w->rank() != 2)
+            throw std::invalid_argument("dense currently only supports rank-2 tensors");
+        if (a->dim(1) != w->dim(0)) throw std::invalid_argument("dense dimension mismatch");
+        if (b && !(b->numel() == static_cast<uint64_t>(w->dim(1)) &&
+                   (b->rank() == 1 || (b->rank() == 2 && b->dim(0) == 1))))
+            throw std::invalid_argument("dense bias must have shape [N] or [1, N]");
+    };
+    check(x, w1, b1);
+    const int64_t M = x->dim(0), K1 = x->dim(1), N1 = w1->dim(1);
+    if (w2->rank() != 2) throw std::invalid_argument("dense currently only supports rank-2 tensors");
+    if (N1 != w2->dim(0)) throw std::invalid_argument("dense dimension mismatch");
+    if (b2 && !(b2->numel() == static_cast<uint64_t>(w2->dim(1)) &&
+                (b2->rank() == 1 || (b2->rank() == 2 && b2->dim(0) == 1))))
+        throw std::invalid_argument("dense bias must have shape [N] or [1, N]");
+    const int64_t N2 = w2->dim(1);
+    auto f32 = [](const TensorObject *t) { return !t || t->dtype() == TypeCode::Float32; };
+    const bool fp32 = x->dtype() == TypeCode::Float32 && f32(w1) && f32(b1) && f32(w2) && f32(b2);
+    if (!fp32 || K1 == 0 || N1 == 0) {
+        TensorObject *h = tensorDense(x, w1, b1, relu1);
+        TensorObject *y = nullptr;
+        try {
+            y = softmax ? tensorDenseSoftmax(h, w2, b2, relu2) : tensorDense(h, w2, b2, relu2);
+        } catch (...) {
+            releaseTensor(h);
+            throw;
+        }
+        releaseTensor(h);
+        return y;
+    }
+    int64_t shape[] = {M, N2};
+    TensorObject *out = deviceTensor(TypeCode::Float32, shape);
+    if (M == 0 || N2 == 0) return out;
+    auto dev = [](const TensorObject *t) {
+        return t ? static_cast<const float *>(t->deviceData()) : nullptr;
+    };
+    checkHip(camel_hip_dense_head(dev(x), dev(w1), dev(b1), dev(w2), dev(b2),
+                                  static_cast<float *>(out->deviceOutput()), M, K1, N1, N2,
+                                  (b1 ? CAMEL_EPI_BIAS : 0) | (relu1 ? CAMEL_EPI_RELU : 0),
+                                  (b2 ? CAMEL_EPI_BIAS : 0) | (relu2 ? CAMEL_EPI_RELU : 0),
+                                  softmax ? 1 : 0));
+    return out;
+}
+
 // conv2d: x [N, C, H, W], w [Co, C, KH, KW], bias [Co] -> y [N, Co, OH, OW],
 // OH = (H + 2 pad - KH) / stride + 1.  Float32 only.
 std::array<int64_t, 4> conv2dOutputShape(std::span<const int64_t> xs, TypeCode xdtype,

@@ -57,13 +57,18 @@ TensorObject *tensorConv2d(const TensorObject *x, const TensorObject *w, const T
 TensorObject *tensorMaxPool2d(const TensorObject *x, int64_t kernel, int64_t stride);
 
 // Fused layer pairs for composed chains (the reference's compose `..` is a
-// stub, src/builtin/operators/macro.cpp:30): dense (relu) then softmax, and
-// conv2d (relu) then maxpool2d(2, 2).  Same checks and error texts as the
-// layers they fuse.
+// stub, src/builtin/operators/macro.cpp:30): dense (relu) then softmax,
+// dense (relu) then a narrow dense (relu, softmax), and conv2d (relu) then
+// maxpool2d(2, 2).  Same checks and error texts as the layers they fuse.
 TensorObject *tensorDenseSoftmax(const TensorObject *x, const TensorObject *w,
                                  const TensorObject *bias, bool relu);
 TensorObject *tensorConv2dPool2(const TensorObject *x, const TensorObject *w,
                                 const TensorObject *bias, int64_t stride, int64_t pad, bool relu);
+// dense (relu) then dense (relu) (then softmax), the two layers of a
+// classifier head; the values of the two layers' functions.
+TensorObject *tensorDenseHead(const TensorObject *x, const TensorObject *w1,
+                              const TensorObject *b1, bool relu1, const TensorObject *w2,
+                              const TensorObject *b2, bool relu2, bool softmax);
 // The conv2d checks (error texts of tensorConv2d) on an input of shape xs and
 // dtype xdtype; returns the NCHW output shape.
 std::array<int64_t, 4> conv2dOutputShape(std::span<const int64_t> xs, TypeCode xdtype,

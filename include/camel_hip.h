@@ -127,6 +127,19 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
  * (`..`, src/builtin/operators/macro.cpp:30) is a stub. */
 int camel_hip_dense_softmax(const float *A, const float *B, const float *bias, float *C, int64_t M,
                             int64_t N, int64_t K, int flags);
+/* y[M,N2] = [softmax_rows]( H . W2 (+b2) (relu) ) with H = x[M,K1] . W1[K1,N1]
+ * (+b1) (relu): the two dense layers of a classifier head
+ * (`dense<w1, b1>..relu..dense<w2, b2>..softmax`, README.md:40-46); flags1 /
+ * flags2 are each layer's CAMEL_EPI_* bits, softmax != 0 adds the row
+ * softmax.  Equals camel_hip_sgemm(x, W1) into H followed by
+ * camel_hip_dense_softmax (softmax) or camel_hip_sgemm (no softmax) on H, bit
+ * for bit.  When layer 1 runs as a split-K GEMM and N2 <= 16, layer 2's kernel
+ * adds layer 1's partial sums itself (no reduce launch, H never reaches HBM).
+ * No reference operator: the reference's compose is a stub
+ * (src/builtin/operators/macro.cpp:30). */
+int camel_hip_dense_head(const float *x, const float *w1, const float *b1, const float *w2,
+                         const float *b2, float *y, int64_t M, int64_t K1, int64_t N1, int64_t N2,
+                         int flags1, int flags2, int softmax);
 /* Mixed-dtype matmul through double (Int64 / Bool operands, promoted output
  * dtype, promoteTensorTypes runtime.cpp:570-580). */
 int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int odt, void *C,

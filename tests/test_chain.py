@@ -29,19 +29,27 @@ def cnn_chain(c1=1, c2=32, c3=64):
 
 def test_cnn_chain_plan_fuses_every_pair():
     # The benchmark small CNN as a chain: conv1 writes NCHW4 for conv2, conv2 + relu
-    # + pool are one kernel, the classifier and the softmax one more.
+    # + pool are one kernel, and the two dense layers with the softmax one head.
     assert cnn_chain().plan((512, 1, 28, 28)) == [
-        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4", "reshape", "dense_relu",
-        "dense+softmax"]
+        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4", "reshape",
+        "dense_relu+dense+softmax"]
 
 
 def test_mlp_chain_plan():
     # README.md:40-46: dense<w1, b1>..relu.., dense<w3, b3>..softmax
     c = T.Chain(("dense", z(784, 1024), z(1024)), "relu", ("dense", z(1024, 1024), z(1024)),
                 "relu", ("dense", z(1024, 10), z(10)), "softmax")
-    assert c.plan((1024, 784)) == ["dense_relu", "dense_relu", "dense+softmax"]
+    assert c.plan((1024, 784)) == ["dense_relu", "dense_relu+dense+softmax"]
     c = T.Chain(("dense_relu", z(8, 4)), "softmax")
     assert c.plan((2, 8)) == ["dense_relu+softmax"]
+    # a head needs a second dense of at most 16 columns; its relu and the
+    # softmax are optional
+    c = T.Chain(("dense", z(8, 6)), ("dense", z(6, 17)), "softmax")
+    assert c.plan((2, 8)) == ["dense", "dense+softmax"]
+    c = T.Chain(("dense", z(8, 6)), ("dense", z(6, 16)), "relu")
+    assert c.plan((2, 8)) == ["dense+dense_relu"]
+    c = T.Chain(("dense_relu", z(8, 6)), ("dense_relu", z(6, 3)), "softmax", "relu")
+    assert c.plan((2, 8)) == ["dense_relu+dense_relu+softmax", "relu"]
 
 
 W = "w"  # a weight tensor of the given shape, made inside the test

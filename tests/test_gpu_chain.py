@@ -36,7 +36,7 @@ def test_mlp_chain_equals_layer_calls():
     bs = [t(D.uniform(0x6005 + i, (dims[i + 1],), -0.1, 0.1)) for i in range(3)]
     chain = T.Chain(("dense", ws[0], bs[0]), "relu", ("dense", ws[1], bs[1]), "relu",
                     ("dense", ws[2], bs[2]), "softmax")
-    assert chain.plan((256, 784)) == ["dense_relu", "dense_relu", "dense+softmax"]
+    assert chain.plan((256, 784)) == ["dense_relu", "dense_relu+dense+softmax"]
     xt = t(x)
     got = chain(xt)
     h = T.call("dense_relu", xt, with_=(ws[0], bs[0]))
@@ -53,7 +53,9 @@ def test_mlp_chain_equals_layer_calls():
 
 
 def test_cnn_chain_equals_layer_calls():
-    # The benchmark small CNN at batch 16: NCHW4 intermediate, fused pool, fused softmax
+    # The benchmark small CNN at batch 16: NCHW4 intermediate, fused pool, the
+    # dense head (at 16 rows layer 1 is the skinny kernel: the head runs as two
+    # calls)
     B = 16
     x = D.uniform(0x6100, (B, 1, 28, 28), 0.0, 1.0)
     w1 = t(D.normal(0x6101, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9))))
@@ -65,8 +67,8 @@ def test_cnn_chain_equals_layer_calls():
     chain = T.Chain(("conv2d_relu", w1, b1), ("conv2d_relu", w2, b2), ("maxpool2d", 2, 2),
                     ("reshape", B, 9216), ("dense_relu", w3, b3), ("dense", w4, b4), "softmax")
     assert chain.plan((B, 1, 28, 28)) == [
-        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4", "reshape", "dense_relu",
-        "dense+softmax"]
+        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4", "reshape",
+        "dense_relu+dense+softmax"]
     xt = t(x)
     got = chain(xt)
     h = T.call("conv2d_relu", xt, with_=(w1, b1))
@@ -76,6 +78,38 @@ def test_cnn_chain_equals_layer_calls():
     h = T.call("dense_relu", h, with_=(w3, b3))
     h = T.call("dense", h, with_=(w4, b4))
     ref = T.call("softmax", h)
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+    chain.release()
+
+
+@pytest.mark.parametrize("M,softmax", [(96, True), (200, False)])
+def test_dense_head_chain_from_split_partials_equals_layer_calls(M, softmax):
+    # The CNN's classifier head at 96 / 200 rows (ragged 64x64 tiles, 36 / 32
+    # K splits): layer 2's kernel rebuilds layer 1's rows from the partials.
+    x = t(D.uniform(0x6600 + M, (M, 9216), 0.0, 1.0))
+    w1 = t(D.normal(0x6601, (9216, 128), std=float(np.sqrt(2.0 / 9216))))
+    w2 = t(D.normal(0x6602, (128, 10), std=float(np.sqrt(2.0 / 128))))
+    b1, b2 = t(D.uniform(0x6603, (128,), -0.1, 0.1)), t(D.uniform(0x6604, (10,), -0.1, 0.1))
+    layers = [("dense_relu", w1, b1), ("dense", w2, b2)] + (["softmax"] if softmax else ["relu"])
+    chain = T.Chain(*layers)
+    assert chain.plan((M, 9216)) == ["dense_relu+dense+softmax" if softmax else "dense_relu+dense_relu"]
+    got = chain(x)
+    h = T.call("dense_relu", x, with_=(w1, b1))
+    h = T.call("dense", h, with_=(w2, b2))
+    ref = T.call("softmax" if softmax else "relu", h)
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+    chain.release()
+
+
+def test_dense_head_chain_int64_follows_the_composition():
+    x = t((np.arange(20).reshape(5, 4) - 7).astype(np.int64))
+    w1 = t((np.arange(12).reshape(4, 3) % 4 - 1).astype(np.int64))
+    w2 = t((np.arange(6).reshape(3, 2) % 3).astype(np.int64))
+    chain = T.Chain(("dense_relu", w1), ("dense", w2), "softmax")
+    assert chain.plan((5, 4)) == ["dense_relu+dense+softmax"]
+    got = chain(x)
+    ref = T.call("softmax", T.call("dense", T.call("dense_relu", x, with_=(w1,)), with_=(w2,)))
+    assert got.dtype_code == ref.dtype_code
     np.testing.assert_array_equal(got.numpy(), ref.numpy())
     chain.release()
 

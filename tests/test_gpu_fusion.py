@@ -5,6 +5,10 @@ unfused device chain and the CPU oracle.
   equals camel_hip_sgemm then camel_hip_softmax_rows bit for bit where the
   fused path serves (N <= 32, one value per lane), and the softmax of the
   device GEMM result per the oracle.
+* dense..relu..dense..softmax: camel_hip_dense_head equals camel_hip_sgemm
+  then camel_hip_dense_softmax (or camel_hip_sgemm) bit for bit, whether
+  layer 2 rebuilds layer 1's rows from its split-K partials or the two
+  layers run as two calls.
 * conv2d layouts: CAMEL_CONV_X_NHWC / CAMEL_CONV_Y_NHWC and
   CAMEL_CONV_X_NCHW4 / CAMEL_CONV_Y_NCHW4 change addressing only, so results
   equal the NCHW conv bit for bit.
@@ -105,6 +109,59 @@ def test_dense_softmax_argument_errors():
     assert lib.camel_hip_dense_softmax(None, None, None, None, -1, 2, 2, 0) == H.ERR_SHAPE
     assert lib.camel_hip_dense_softmax(None, None, None, None, 2, 2, 2, H.EPI_BIAS) == H.ERR_ARG
     assert lib.camel_hip_dense_softmax(None, None, None, None, 0, 2, 2, 0) == 0
+
+
+# ------------------------------------------------------------------ dense head
+
+def _dense_head(x, w1, b1, w2, b2, flags1, flags2, softmax):
+    M, K1 = x.shape
+    N1, N2 = w1.shape[1], w2.shape[1]
+    dx, dw1, dw2, dy = K.dev(x), K.dev(w1), K.dev(w2), K.empty(M * N2 * 4)
+    db1, db2 = K.dev(b1), K.dev(b2)
+    H.call("camel_hip_dense_head", P(dx.ptr), P(dw1.ptr), P(db1.ptr), P(dw2.ptr), P(db2.ptr),
+           P(dy.ptr), M, K1, N1, N2, flags1, flags2, int(softmax))
+    return K.host(dy, F, (M, N2))
+
+
+def _head_in_two_calls(x, w1, b1, w2, b2, flags1, flags2, softmax):
+    h = K.sgemm(x, w1, b1, flags1)
+    if softmax:
+        return h, _dense_softmax(h, w2, b2, flags2)
+    return h, K.sgemm(h, w2, b2, flags2)
+
+
+@pytest.mark.parametrize("M,K1,N1,N2,flags2,softmax", [
+    (512, 9216, 128, 10, H.EPI_BIAS, True),             # the benchmark CNN's head (16 K splits)
+    (512, 9216, 128, 10, H.EPI_BIAS | H.EPI_RELU, False),
+    (300, 2000, 200, 16, H.EPI_BIAS, True),             # ragged tiles, N2 = 16
+    (130, 700, 72, 5, 0, True),                         # 32x32 tiles with K splits
+    (1024, 1024, 1024, 10, H.EPI_BIAS, True),           # the MLP's head: no split, two calls
+    (257, 300, 24, 9, H.EPI_BIAS, True),                # layer 1 on the thin-N kernel, two calls
+])
+def test_dense_head_equals_two_calls(M, K1, N1, N2, flags2, softmax):
+    x = D.uniform(0x5400 + M, (M, K1), 0.0, 1.0)
+    w1 = D.normal(0x5401 + N1, (K1, N1), std=float(np.sqrt(2.0 / K1)))
+    b1 = D.uniform(0x5402, (N1,), -0.1, 0.1)
+    w2 = D.normal(0x5403 + N2, (N1, N2), std=float(np.sqrt(2.0 / N1)))
+    b2 = D.uniform(0x5404, (N2,), -0.1, 0.1)
+    flags1 = H.EPI_BIAS | H.EPI_RELU
+    got = _dense_head(x, w1, b1, w2, b2, flags1, flags2, softmax)
+    h, ref = _head_in_two_calls(x, w1, b1, w2, b2, flags1, flags2, softmax)
+    np.testing.assert_array_equal(got, ref)
+    # and layer 1 itself against the oracle's dense (the GEMM tolerance)
+    rows = slice(0, 8)
+    ok, worst = K.gemm_tol_ok(h[rows], O.dense(x[rows], w1, b1, True), x[rows], w1)
+    assert ok, f"layer 1 worst error / bound = {worst}"
+
+
+def test_dense_head_argument_errors():
+    lib = H.load()
+    z = (None,) * 6
+    assert lib.camel_hip_dense_head(*z, -1, 2, 2, 2, 0, 0, 0) == H.ERR_SHAPE
+    assert lib.camel_hip_dense_head(*z, 2, 2, 2, 2, H.EPI_BIAS, 0, 0) == H.ERR_ARG
+    assert lib.camel_hip_dense_head(*z, 2, 2, 2, 2, 0, 0x100, 0) == H.ERR_ARG
+    assert lib.camel_hip_dense_head(*z, 2, 2, 2, 2, 0, 0, 0) == H.ERR_ARG  # null operands
+    assert lib.camel_hip_dense_head(*z, 0, 2, 2, 2, 0, 0, 1) == 0
 
 
 # ------------------------------------------------------------------ conv2d layouts
