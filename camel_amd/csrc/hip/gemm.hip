@@ -786,19 +786,20 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 // POOL (pooled conv): one thread per pool window (4 consecutive columns of
 // a tile), max of the 4 finished values in window order.
 // sum_z partial[z * total + idx] for z = 0 .. splits-1, added in split order;
-// loads go out 8 at a time so their latencies overlap.
+// loads go out up to 8 at a time (the guards are uniform) so their latencies
+// overlap instead of each add waiting for its load.
 __device__ __forceinline__ float sum_splits(const float *__restrict__ partial, size_t total,
                                             size_t idx, int splits) {
     float s = partial[idx];
-    int z = 1;
-    for (; z + 8 <= splits; z += 8) {
+    for (int z0 = 1; z0 < splits; z0 += 8) {
         float t[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) t[u] = partial[(size_t)(z + u) * total + idx];
+        for (int u = 0; u < 8; ++u)
+            if (z0 + u < splits) t[u] = partial[(size_t)(z0 + u) * total + idx];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s = s + t[u];
+        for (int u = 0; u < 8; ++u)
+            if (z0 + u < splits) s = s + t[u];
     }
-    for (; z < splits; ++z) s = s + partial[(size_t)z * total + idx];
     return s;
 }
 
@@ -1289,13 +1290,22 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float4 *__rest
     const size_t total4 = (size_t)M * N / 4;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= total4) return;
+    // k groups added in order; their loads go out up to 8 at a time
     float4 y = partial[idx];
-    for (int z = 1; z < nks; ++z) {
-        const float4 p = partial[(size_t)z * total4 + idx];
-        y.x = y.x + p.x;
-        y.y = y.y + p.y;
-        y.z = y.z + p.z;
-        y.w = y.w + p.w;
+    for (int z0 = 1; z0 < nks; z0 += 8) {
+        float4 p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (z0 + u < nks) p[u] = partial[(size_t)(z0 + u) * total4 + idx];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (z0 + u < nks) {
+                y.x = y.x + p[u].x;
+                y.y = y.y + p[u].y;
+                y.z = y.z + p[u].z;
+                y.w = y.w + p[u].w;
+            }
+        }
     }
     if (flags & CAMEL_EPI_BIAS) {
         const size_t col = (idx * 4) % (size_t)N;
