@@ -1760,7 +1760,7 @@ int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char 
     g.k_per_split = std::max(1, kps_stages) * T::BK;
     splits = std::max(1, (g.K + g.k_per_split - 1) / g.k_per_split);
     g.partial = nullptr;
-    if (splits > 1) {
+    if (splits > 1 || partials_only) { // a partials-only launch writes partials even unsplit
         CAMEL_RETURN_IF(
             ensure_partial((size_t)splits * ntiles * T::BM * T::BN * sizeof(float)));
         g.partial = g_partial;
