@@ -101,6 +101,25 @@ def test_dense_head_chain_from_split_partials_equals_layer_calls(M, softmax):
     chain.release()
 
 
+def test_dense_head_chain_errors_match_the_failing_layer():
+    x = t(D.uniform(0x6700, (40, 8), -1.0, 1.0))
+    w1 = t(D.normal(0x6701, (8, 6), std=0.3))
+    bad_w2 = t(np.zeros((7, 3), F))
+    chain = T.Chain(("dense_relu", w1), ("dense", bad_w2), "softmax")
+    assert chain.plan((40, 8)) == ["dense_relu+dense+softmax"]
+    with pytest.raises(T.CamelError, match="dense dimension mismatch"):
+        chain(x)
+    w2 = t(np.zeros((6, 3), F))
+    bad_b2 = t(np.zeros((4,), F))
+    chain2 = T.Chain(("dense_relu", w1), ("dense", w2, bad_b2))
+    with pytest.raises(T.CamelError, match=r"dense bias must have shape \[N\] or \[1, N\]"):
+        chain2(x)
+    with pytest.raises(T.CamelError, match="dense dimension mismatch"):
+        chain2(t(np.zeros((40, 5), F)))  # layer 1's error comes first
+    for c in (chain, chain2):
+        c.release()
+
+
 def test_dense_head_chain_int64_follows_the_composition():
     x = t((np.arange(20).reshape(5, 4) - 7).astype(np.int64))
     w1 = t((np.arange(12).reshape(4, 3) % 4 - 1).astype(np.int64))
