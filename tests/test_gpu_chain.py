@@ -52,6 +52,32 @@ def test_mlp_chain_equals_layer_calls():
     chain.release()
 
 
+def test_mlp_chain_full_batch_against_the_oracle():
+    # BASELINE config 2 at its full batch (1024): every row a probability
+    # vector, and rows from the first, a middle and the last tile row within
+    # 1e-4 of the oracle's dense layers and softmax (device and oracle logits
+    # differ by the GEMM bound, about 1e-6 here, and a softmax output moves by
+    # no more than its largest input change).
+    dims = [784, 1024, 1024, 10]
+    x = D.uniform(D.SEED_MLP, (1024, 784), 0.0, 1.0)
+    wn = [D.normal(D.SEED_MLP + 1 + i, (dims[i], dims[i + 1]), std=float(np.sqrt(1.0 / dims[i])))
+          for i in range(3)]
+    bn = [D.uniform(0x6800 + i, (dims[i + 1],), -0.05, 0.05) for i in range(3)]
+    ws, bs = [t(w) for w in wn], [t(b) for b in bn]
+    chain = T.Chain(("dense_relu", ws[0], bs[0]), ("dense_relu", ws[1], bs[1]),
+                    ("dense", ws[2], bs[2]), "softmax")
+    got = chain(t(x)).numpy()
+    np.testing.assert_allclose(got.sum(axis=1, dtype=np.float64), 1.0, rtol=0, atol=1e-5)
+    for r0, r1 in ((0, 4), (510, 514), (1020, 1024)):
+        h = x[r0:r1]
+        for i in range(2):
+            h = O.dense(h, wn[i], bn[i], True)
+        logits = O.dense(h, wn[2], bn[2], False)
+        p = O.softmax_rows(logits)
+        assert np.max(np.abs(got[r0:r1] - p)) <= 1e-4
+    chain.release()
+
+
 def test_cnn_chain_equals_layer_calls():
     # The benchmark small CNN at batch 16: NCHW4 intermediate, fused pool, the
     # dense head (at 16 rows layer 1 is the skinny kernel: the head runs as two

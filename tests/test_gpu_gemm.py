@@ -99,6 +99,25 @@ def test_dense_bias_relu_matches_oracle(M, N, Kd):
     assert np.all(np.signbit(got[(got == 0) & neg]))
 
 
+def test_gemm_8192_row_sums_and_slab():
+    # The largest square config at full size: every row's sum checked through
+    # C 1 = A (B 1) in fp64 (size-independent: a dropped or repeated k term,
+    # tile or split shows up in its row), plus 4 rows against the oracle.
+    n = 8192
+    a, b = _ab(n, n, n, D.SEED_GEMM + n)
+    got = K.sgemm(a, b)
+    bv = b.astype(np.float64).sum(axis=1)
+    ref_sums = a.astype(np.float64) @ bv
+    # bound: the per-element GEMM bound summed over the row
+    mag = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64)).sum(axis=1)
+    err = np.abs(got.astype(np.float64).sum(axis=1) - ref_sums)
+    assert np.all(err <= 1e-5 * np.sqrt(n) * mag + n * 1e-30)
+    for r0 in (0, n - 4):
+        ref = O.matmul_rows(a, b, r0, r0 + 4)
+        ok, worst = K.gemm_tol_ok(got[r0:r0 + 4], ref, a[r0:r0 + 4], b)
+        assert ok, f"rows {r0}+4: worst error / bound = {worst}"
+
+
 @pytest.mark.parametrize("n", [1024, 2048, 4096])
 def test_square_gemm_row_slab(n):
     a, b = _ab(n, n, n, D.SEED_GEMM + n)
