@@ -108,6 +108,35 @@ def test_cnn_chain_equals_layer_calls():
     chain.release()
 
 
+def test_cnn_chain_full_batch_against_the_oracle():
+    # BASELINE config 5 at its full batch (512), the benchmarked path: NCHW4
+    # between the convs, pooled conv2, and the dense head whose second layer
+    # adds dense1's 16 K splits.  Every row a probability vector; images 0,
+    # 255 and 511 within 1e-4 of the oracle's layers (conv, pool, dense,
+    # softmax).
+    B = 512
+    x = D.uniform(D.SEED_CNN, (B, 1, 28, 28), 0.0, 1.0)
+    wn = [D.normal(D.SEED_CNN + 1, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9))),
+          D.normal(D.SEED_CNN + 2, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288))),
+          D.normal(D.SEED_CNN + 3, (9216, 128), std=float(np.sqrt(2.0 / 9216))),
+          D.normal(D.SEED_CNN + 4, (128, 10), std=float(np.sqrt(2.0 / 128)))]
+    bn = [D.uniform(0x6900 + i, (n,), -0.05, 0.05) for i, n in enumerate((32, 64, 128, 10))]
+    w, b = [t(a) for a in wn], [t(a) for a in bn]
+    chain = T.Chain(("conv2d_relu", w[0], b[0]), ("conv2d_relu", w[1], b[1]), ("maxpool2d", 2, 2),
+                    ("reshape", B, 9216), ("dense_relu", w[2], b[2]), ("dense", w[3], b[3]),
+                    "softmax")
+    got = chain(t(x)).numpy()
+    np.testing.assert_allclose(got.sum(axis=1, dtype=np.float64), 1.0, rtol=0, atol=1e-5)
+    for n in (0, 255, 511):
+        h = O.conv2d_images(x, wn[0], bn[0], True, n, n + 1)
+        h = O.conv2d(h, wn[1], bn[1], True)
+        h = O.maxpool2d(h, 2, 2).reshape(1, 9216)
+        h = O.dense(h, wn[2], bn[2], True)
+        p = O.softmax_rows(O.dense(h, wn[3], bn[3], False))
+        assert np.max(np.abs(got[n:n + 1] - p)) <= 1e-4, f"image {n}"
+    chain.release()
+
+
 @pytest.mark.parametrize("M,softmax", [(96, True), (200, False)])
 def test_dense_head_chain_from_split_partials_equals_layer_calls(M, softmax):
     # The CNN's classifier head at 96 / 200 rows (ragged 64x64 tiles, 36 / 32
