@@ -47,6 +47,25 @@ def test_hip_abi_exports_every_declared_symbol():
     assert declared == set(H.exported_symbols())
 
 
+def test_hip_abi_rejects_extents_whose_products_overflow():
+    # Shape checks run before the library touches the device, so these calls
+    # need no GPU.  Each case's element count wraps around int64 (or around
+    # to a small value) if multiplied unchecked.
+    lib = H.load()
+    big = 2**32
+    conv = lib.camel_hip_conv2d
+    assert conv(None, None, None, None, 1, 2**31 - 1, 2**31 - 1, 2**31 - 1, 8, 1, 1, 1, 0,
+                0) == H.ERR_SHAPE
+    assert conv(None, None, None, None, 1, 8, 8, 8, big, 1, 1, 1, 0, 0) == H.ERR_SHAPE
+    assert conv(None, None, None, None, 1, 8, 8, 8, 8, 3, 3, 1, 2**62, 0) == H.ERR_SHAPE
+    assert lib.camel_hip_conv2d_pool2(None, None, None, None, big, big, 8, 8, 8, 3, 3, 1, 0,
+                                      0) == H.ERR_SHAPE
+    # Co * C = 2**64 wraps to 0: a wrapped product would pass as an empty tensor.
+    assert lib.camel_hip_conv2d_pack_weights(None, None, big, big, 1, 1) == H.ERR_SHAPE
+    assert lib.camel_hip_conv2d_pack_weights(None, None, 2**31, 1, 1, 1) == H.ERR_SHAPE
+    assert b"too large" in lib.camel_hip_last_error()
+
+
 def test_tensor_abi_exports_every_declared_symbol():
     lib = T.load()
     declared = declared_functions("camel_tensor.h")
