@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 
@@ -36,6 +37,15 @@ int *error_flag();
 int clear_error_flag();
 // Reads the flag; returns its value through `value`.
 int read_error_flag(int *value);
+
+// True when the product of non-negative factors is at most `limit`, checked
+// at every step so that huge factors cannot wrap around into range.
+inline bool product_fits(std::initializer_list<int64_t> factors, int64_t limit = INT32_MAX) {
+    int64_t p = 1;
+    for (int64_t f : factors)
+        if (__builtin_mul_overflow(p, f, &p) || p > limit) return false;
+    return true;
+}
 
 // Bytes of one element of a storage dtype (0 for an unknown dtype).
 inline size_t dtype_size(int dt) {

@@ -35,7 +35,6 @@
 #include "row_softmax.h"
 
 #include <algorithm>
-#include <initializer_list>
 #include <type_traits>
 #include <vector>
 
@@ -2150,15 +2149,6 @@ int conv2d_gather(const float *x, const float *w, const float *bias, float *y, i
     return ok();
 }
 
-// True when the product of non-negative factors fits int32 (checked at every
-// step, so huge factors cannot wrap around into range).
-bool product_fits_i32(std::initializer_list<int64_t> factors) {
-    int64_t p = 1;
-    for (int64_t f : factors)
-        if (__builtin_mul_overflow(p, f, &p) || p > INT32_MAX) return false;
-    return true;
-}
-
 // Shared argument checks of the conv2d entry points.
 int conv_check(const float *x, const float *w, const float *bias, const float *y, int64_t N,
                int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW, int64_t stride,
@@ -2176,8 +2166,8 @@ int conv_check(const float *x, const float *w, const float *bias, const float *y
         return fail(CAMEL_HIP_ERR_SHAPE, name + ": kernel larger than padded input");
     if (KH > 0xffff || KW > 0xffff) return fail(CAMEL_HIP_ERR_SHAPE, name + ": kernel too large");
     const int64_t OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
-    if (!product_fits_i32({N, C, H, W}) || !product_fits_i32({N, OH, OW}) ||
-        !product_fits_i32({N, Co, OH, OW}) || !product_fits_i32({Co, C, KH, KW}))
+    if (!product_fits({N, C, H, W}) || !product_fits({N, OH, OW}) ||
+        !product_fits({N, Co, OH, OW}) || !product_fits({Co, C, KH, KW}))
         return fail(CAMEL_HIP_ERR_SHAPE, name + ": tensor too large");
     if (flags & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU | CAMEL_CONV_X_NHWC | CAMEL_CONV_Y_NHWC |
                   CAMEL_CONV_W_PACKED | CAMEL_CONV_X_NCHW4 | CAMEL_CONV_Y_NCHW4))
@@ -2471,7 +2461,7 @@ int camel_hip_conv2d(const float *x, const float *w, const float *bias, float *y
 int camel_hip_conv2d_pack_weights(const float *w, float *wp, int64_t Co, int64_t C, int64_t KH,
                                   int64_t KW) {
     if (Co < 0 || C < 0 || KH < 0 || KW < 0) return fail(CAMEL_HIP_ERR_SHAPE, "conv2d_pack_weights: negative dimension");
-    if (!product_fits_i32({Co, C, KH, KW}))
+    if (!product_fits({Co, C, KH, KW}))
         return fail(CAMEL_HIP_ERR_SHAPE, "conv2d_pack_weights: tensor too large");
     if (Co * C * KH * KW == 0) return ok();
     if (!w || !wp) return fail(CAMEL_HIP_ERR_ARG, "conv2d_pack_weights: null pointer");

@@ -116,6 +116,9 @@ int camel_hip_concat(int dt, const void *l, const void *r, void *out, int64_t ou
     if (!valid_dtype(dt)) return fail(CAMEL_HIP_ERR_DTYPE, "concat: unsupported dtype");
     if (outer < 0 || l_axis < 0 || r_axis < 0 || inner < 0)
         return fail(CAMEL_HIP_ERR_SHAPE, "concat: negative extent");
+    if (!product_fits({outer, l_axis, inner, 8}, INT64_MAX / 2) ||
+        !product_fits({outer, r_axis, inner, 8}, INT64_MAX / 2))
+        return fail(CAMEL_HIP_ERR_SHAPE, "concat: tensor too large");
     const size_t item = dtype_size(dt);
     const size_t lw = (size_t)(l_axis * inner) * item, rw = (size_t)(r_axis * inner) * item;
     const size_t ow = lw + rw;
@@ -139,7 +142,7 @@ int camel_hip_maxpool2d(const float *x, float *y, int64_t N, int64_t C, int64_t 
     if (N < 0 || C < 0 || H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || stride <= 0 || H < KH ||
         W < KW)
         return fail(CAMEL_HIP_ERR_SHAPE, "maxpool2d: invalid geometry");
-    if (H > INT32_MAX / 2 || W > INT32_MAX / 2)
+    if (H > INT32_MAX / 2 || W > INT32_MAX / 2 || !product_fits({N, C, H, W}, INT64_MAX / 4))
         return fail(CAMEL_HIP_ERR_SHAPE, "maxpool2d: tensor too large");
     const int64_t OH = (H - KH) / stride + 1, OW = (W - KW) / stride + 1;
     const int64_t planes = N * C;

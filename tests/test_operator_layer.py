@@ -64,6 +64,10 @@ def test_hip_abi_rejects_extents_whose_products_overflow():
     assert lib.camel_hip_conv2d_pack_weights(None, None, big, big, 1, 1) == H.ERR_SHAPE
     assert lib.camel_hip_conv2d_pack_weights(None, None, 2**31, 1, 1, 1) == H.ERR_SHAPE
     assert b"too large" in lib.camel_hip_last_error()
+    assert lib.camel_hip_maxpool2d(None, None, big, big, 8, 8, 2, 2, 2) == H.ERR_SHAPE
+    assert lib.camel_hip_concat(H.DT_I64, None, None, None, big, big, 1, 2) == H.ERR_SHAPE
+    assert lib.camel_hip_concat(H.DT_I64, None, None, None, 2, 1, 2**62, 1) == H.ERR_SHAPE
+    assert b"too large" in lib.camel_hip_last_error()
 
 
 def test_tensor_abi_exports_every_declared_symbol():
