@@ -242,6 +242,8 @@ template <int ITEMS> int launch_softmax(const float *x, float *y, int64_t rows, 
 
 int check_axis(int64_t rows, int64_t cols, int64_t &axis, const char *what) {
     if (rows < 0 || cols < 0) return fail(CAMEL_HIP_ERR_SHAPE, std::string(what) + ": negative shape");
+    if (!product_fits({rows, cols, 8}, INT64_MAX))
+        return fail(CAMEL_HIP_ERR_SHAPE, std::string(what) + ": tensor too large");
     if (axis < 0) axis += 2;
     if (axis != 0 && axis != 1)
         return fail(CAMEL_HIP_ERR_SHAPE,
@@ -282,6 +284,8 @@ extern "C" {
 
 int camel_hip_softmax_rows(const float *x, float *y, int64_t rows, int64_t cols) {
     if (rows < 0 || cols < 0) return fail(CAMEL_HIP_ERR_SHAPE, "softmax: negative shape");
+    if (!product_fits({rows, cols, 4}, INT64_MAX))
+        return fail(CAMEL_HIP_ERR_SHAPE, "softmax: tensor too large");
     if (rows == 0 || cols == 0) return ok();
     if (!x || !y) return fail(CAMEL_HIP_ERR_ARG, "softmax: null pointer");
     if (cols > INT32_MAX / 2) return fail(CAMEL_HIP_ERR_SHAPE, "softmax: row too long");

@@ -68,6 +68,10 @@ def test_hip_abi_rejects_extents_whose_products_overflow():
     assert lib.camel_hip_concat(H.DT_I64, None, None, None, big, big, 1, 2) == H.ERR_SHAPE
     assert lib.camel_hip_concat(H.DT_I64, None, None, None, 2, 1, 2**62, 1) == H.ERR_SHAPE
     assert b"too large" in lib.camel_hip_last_error()
+    assert lib.camel_hip_sum_axis(H.DT_F32, None, big, big, 0, None) == H.ERR_SHAPE
+    assert lib.camel_hip_argmax_axis(H.DT_I64, None, 2**61, 2, 1, None) == H.ERR_SHAPE
+    assert lib.camel_hip_softmax_rows(None, None, 2**62, 4) == H.ERR_SHAPE
+    assert b"too large" in lib.camel_hip_last_error()
 
 
 def test_tensor_abi_exports_every_declared_symbol():
