@@ -49,6 +49,7 @@ _SIGNATURES = {
     "camel_hip_current_device": [C.POINTER(_I)],
     "camel_hip_last_error": [],
     "camel_hip_sync": [],
+    "camel_hip_device_sync": [],
     "camel_hip_stream": [],
     "camel_hip_malloc": [C.POINTER(_P), C.c_size_t],
     "camel_hip_free": [_P],

@@ -1326,8 +1326,8 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float4 *__rest
 // Mixed-dtype matmul: one thread per output, double accumulation in k order
 // exactly as operators.cpp:757-766, rounded through setFromDouble.
 __global__ void matmul_generic_kernel(int adt, const void *A, int bdt, const void *B, int odt,
-                                      void *C, int M, int N, int K) {
-    const int64_t total = (int64_t)M * N;
+                                      void *C, int64_t M, int64_t N, int64_t K) {
+    const int64_t total = M * N;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
         const int64_t i = idx / N, j = idx % N;
@@ -2437,12 +2437,17 @@ int camel_hip_matmul_generic(int adt, const void *A, int bdt, const void *B, int
     if (!valid_dtype(adt) || !valid_dtype(bdt) || !valid_dtype(odt))
         return fail(CAMEL_HIP_ERR_DTYPE, "matmul: unsupported dtype");
     if (M < 0 || N < 0 || K < 0) return fail(CAMEL_HIP_ERR_SHAPE, "matmul: negative dimension");
+    // Element offsets are int64 in the kernel; every operand's byte count
+    // must fit too (8-byte elements at most).
+    if (!product_fits({M, K, 8}, INT64_MAX) || !product_fits({K, N, 8}, INT64_MAX) ||
+        !product_fits({M, N, 8}, INT64_MAX))
+        return fail(CAMEL_HIP_ERR_SHAPE, "matmul: tensor too large");
     if (M == 0 || N == 0) return ok();
     if (!C || (K > 0 && (!A || !B))) return fail(CAMEL_HIP_ERR_ARG, "matmul: null operand");
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
     hipLaunchKernelGGL(matmul_generic_kernel, dim3(grid_for(M * N, 256)), dim3(256), 0, stream(),
-                       adt, A, bdt, B, odt, C, (int)M, (int)N, (int)K);
+                       adt, A, bdt, B, odt, C, M, N, K);
     CAMEL_RETURN_IF(check_launch("matmul_generic_kernel"));
     return ok();
 }

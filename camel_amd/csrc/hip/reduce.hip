@@ -34,14 +34,8 @@ constexpr int WAVE = 64;
 // past the end of the row hold -inf, which never wins the max and adds an
 // exact 0 to the sum, so only the loads and stores are guarded.
 template <int ITEMS, bool VEC>
-__global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restrict__ x,
-                                                           float *__restrict__ y, int64_t rows,
-                                                           int cols) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const float *xr = x + row * cols;
-    float *yr = y + row * cols;
+__device__ __forceinline__ void softmax_row(const float *__restrict__ xr, float *__restrict__ yr,
+                                            int cols, int lane) {
     constexpr int NV = ITEMS * 4;
     float v[NV];
     if constexpr (VEC) {
@@ -99,13 +93,36 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restri
     }
 }
 
+// Row indices of the one-wave-per-row kernels: a grid of at most
+// ROW_GRID_CAP blocks of 4 waves strides over the rows, so any row count
+// fits the launch's 32-bit grid (one row per wave up to 4 * ROW_GRID_CAP rows).
+constexpr int64_t ROW_GRID_CAP = 1 << 20;
+
+inline unsigned row_grid(int64_t rows) {
+    return (unsigned)std::min<int64_t>((rows + 3) / 4, ROW_GRID_CAP);
+}
+
+__device__ __forceinline__ int64_t first_row() {
+    return (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
+}
+
+__device__ __forceinline__ int64_t row_step() { return (int64_t)gridDim.x * (blockDim.x / WAVE); }
+
+template <int ITEMS, bool VEC>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float *__restrict__ x,
+                                                           float *__restrict__ y, int64_t rows,
+                                                           int cols) {
+    const int lane = threadIdx.x & 63;
+    for (int64_t row = first_row(); row < rows; row += row_step())
+        softmax_row<ITEMS, VEC>(x + row * cols, y + row * cols, cols, lane);
+}
+
 // Rows longer than the register budget: max pass, sum pass, write pass.
 __global__ __launch_bounds__(256) void softmax_rows_long_kernel(const float *__restrict__ x,
                                                                 float *__restrict__ y,
                                                                 int64_t rows, int64_t cols) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    for (int64_t row = first_row(); row < rows; row += row_step()) {
     const float *xr = x + row * cols;
     float *yr = y + row * cols;
     float m = -INFINITY;
@@ -119,21 +136,21 @@ __global__ __launch_bounds__(256) void softmax_rows_long_kernel(const float *__r
     s = wave_sum(s);
     const double rcp = 1.0 / (double)(float)s;
     for (int64_t c = lane; c < cols; c += WAVE) yr[c] = softmax_div(softmax_exp(xr[c], mb), rcp);
+    }
 }
 
 // axis = 1: one wave per row.  kind 0 = sum, 1 = max, 2 = argmax.
 __global__ __launch_bounds__(256) void reduce_rows_kernel(int kind, int dt, const void *x,
                                                           int64_t rows, int64_t cols, void *out) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    for (int64_t row = first_row(); row < rows; row += row_step()) {
     const int64_t base = row * cols;
     if (kind == 0) {
         double s = 0.0;
         for (int64_t c = lane; c < cols; c += WAVE) s += load_as_double(dt, x, base + c);
         s = wave_sum(s);
         if (lane == 0) static_cast<float *>(out)[row] = (float)s;
-        return;
+        continue;
     }
     // Values compare as doubles (exact for fp32 and bool; int64 as the
     // reference converts it).  Track them as double to keep int64 order.
@@ -166,6 +183,7 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(int kind, int dt, cons
             static_cast<float *>(out)[row] = (float)bv;
         else
             static_cast<int64_t *>(out)[row] = bi;
+    }
     }
 }
 
@@ -230,7 +248,7 @@ __global__ __launch_bounds__(256) void sum_final_kernel(const double *partial, i
 }
 
 template <int ITEMS> int launch_softmax(const float *x, float *y, int64_t rows, int cols, bool vec) {
-    dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    dim3 grid(row_grid(rows)), block(256);
     if (vec)
         hipLaunchKernelGGL((softmax_rows_kernel<ITEMS, true>), grid, block, 0, stream(), x, y, rows,
                            cols);
@@ -264,7 +282,7 @@ int reduce_axis(int kind, int dt, const void *x, int64_t rows, int64_t cols, int
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
     if (axis == 1) {
-        hipLaunchKernelGGL(reduce_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+        hipLaunchKernelGGL(reduce_rows_kernel, dim3(row_grid(rows)), dim3(256), 0,
                            stream(), kind, dt, x, rows, cols, out);
         CAMEL_RETURN_IF(check_launch("reduce_rows_kernel"));
     } else {
@@ -304,7 +322,7 @@ int camel_hip_softmax_rows(const float *x, float *y, int64_t rows, int64_t cols)
     else if (cols <= 64 * 64)
         CAMEL_RETURN_IF(launch_softmax<16>(x, y, rows, c, vec));
     else {
-        hipLaunchKernelGGL(softmax_rows_long_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+        hipLaunchKernelGGL(softmax_rows_long_kernel, dim3(row_grid(rows)), dim3(256), 0,
                            stream(), x, y, rows, cols);
         CAMEL_RETURN_IF(check_launch("softmax_rows_long_kernel"));
     }

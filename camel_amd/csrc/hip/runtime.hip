@@ -183,6 +183,13 @@ int camel_hip_sync(void) {
     return ok();
 }
 
+int camel_hip_device_sync(void) {
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    CAMEL_RETURN_IF(check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize"));
+    return ok();
+}
+
 int camel_hip_current_device(int *device) {
     if (!device) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_current_device: null pointer");
     CAMEL_LOCK();

@@ -134,17 +134,33 @@ class Context {};
 
 using operator_t = slot_t (*)(ArgsView &with, ArgsView &norm, Context &ctx);
 
+// The type a resolver gives an operator's result: its type code plus the
+// parameter the reference's Type object carries for composite results -- a
+// Tensor's element dtype (TensorType::Dynamic(dtype), modules/tensor/
+// operators.cpp:41-43) or an Array's element type (intArrayType(), 45-48).
+// For other results elem == code.
+struct ResultType {
+    TypeCode code;
+    TypeCode elem;
+    bool operator==(const ResultType &) const = default;
+};
+inline ResultType tensorResult(TypeCode dtype = TypeCode::Float32) {
+    return {TypeCode::Tensor, dtype};
+}
+inline ResultType scalarResult(TypeCode code) { return {code, code}; }
+inline ResultType arrayResult(TypeCode elem) { return {TypeCode::Array, elem}; }
+
 // OperatorGroup: a name and its overloads, tried in order; the first resolver
 // that accepts the argument type codes wins (include/camel/core/operator.h:
-// 87-110, 297-307).  The resolver returns the result type code.
-using resolver_t = std::function<std::optional<TypeCode>(const std::vector<TypeCode> &with,
-                                                         const std::vector<TypeCode> &norm)>;
+// 87-110, 297-307).  The resolver returns the result type.
+using resolver_t = std::function<std::optional<ResultType>(const std::vector<TypeCode> &with,
+                                                           const std::vector<TypeCode> &norm)>;
 struct OperatorGroup {
     std::string name;
     std::vector<std::pair<std::string, resolver_t>> overloads; // {uri, resolver}
 
     // Returns the URI of the first matching overload and its result type.
-    std::optional<std::pair<std::string, TypeCode>>
+    std::optional<std::pair<std::string, ResultType>>
     resolve(const std::vector<TypeCode> &with, const std::vector<TypeCode> &norm) const {
         for (const auto &[uri, fn] : overloads) {
             if (auto t = fn(with, norm)) return std::make_pair(uri, *t);

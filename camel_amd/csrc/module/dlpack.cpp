@@ -3,13 +3,17 @@
 // The reference copies in both directions and handles host memory only.
 // Here a tensor can also be exported without a copy from HBM (kDLROCM): the
 // managed tensor holds a reference to the payload's Storage, so the device
-// block outlives the tensor handle until the consumer's deleter runs.  Imports
+// block outlives the tensor handle until the consumer's deleter runs, and the
+// Storage is marked shared, so its release waits for every stream of the
+// device before the block can be reused (the consumer reads it on its own
+// streams).  Imports
 // copy, from host memory or from device memory on the library's device.
 #include "tensor_object.h"
 
 #include "camel_hip.h"
 
 #include <cstring>
+#include <mutex>
 #include <stdexcept>
 #include <vector>
 
@@ -71,6 +75,10 @@ DLManagedTensor *tensorToDLPack(const TensorObject *tensor, bool onDevice) {
     if (onDevice) {
         data = const_cast<void *>(tensor->deviceData());
         ctx->storage = tensor->storage();
+        {
+            std::lock_guard<std::mutex> lock(ctx->storage->mutex);
+            ctx->storage->shared = true;
+        }
         device = DLDevice{kDLROCM, libraryDevice()};
         // The consumer may read on any stream: finish every pending writer.
         checkHip(camel_hip_sync());

@@ -8,6 +8,7 @@
 #include "chain.h"
 #include "operators.h"
 #include "runtime.h"
+#include "tensor_type.h"
 
 #include <algorithm>
 #include <memory>
@@ -101,7 +102,52 @@ extern "C" {
 
 const char *camel_tensor_last_error(void) { return t_error.c_str(); }
 
-int camel_tensor_abi_version(void) { return 1; }
+int camel_module_abi_version(void) { return 1; }
+
+namespace {
+
+// A TensorType from C-ABI arguments (shape extents must be non-negative).
+bool tensorTypeOf(uint32_t dtype, int64_t rank, const int64_t *shape, TensorType &out) {
+    if (rank < 0 || (rank > 0 && !shape)) return false;
+    std::vector<size_t> dims;
+    for (int64_t i = 0; i < rank; ++i) {
+        if (shape[i] < 0) return false;
+        dims.push_back(static_cast<size_t>(shape[i]));
+    }
+    out = TensorType(std::move(dims), static_cast<TypeCode>(dtype));
+    return true;
+}
+
+} // namespace
+
+int camel_tensor_type_string(uint32_t dtype, int64_t rank, const int64_t *shape, int mangled,
+                             char *buf, size_t cap, size_t *needed) {
+    TensorType t;
+    if (!tensorTypeOf(dtype, rank, shape, t))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_type_string: bad shape");
+    return guarded([&] {
+        const std::string text = mangled ? t.mangle() : t.toString();
+        if (needed) *needed = text.size() + 1;
+        if (buf && cap > 0) {
+            const size_t n = std::min(cap - 1, text.size());
+            std::memcpy(buf, text.data(), n);
+            buf[n] = '\0';
+        }
+        return ok();
+    });
+}
+
+int camel_tensor_type_relation(uint32_t dst_dtype, int64_t dst_rank, const int64_t *dst_shape,
+                               uint32_t src_dtype, int64_t src_rank, const int64_t *src_shape,
+                               int *assignable, int *equal) {
+    TensorType dst, src;
+    if (!tensorTypeOf(dst_dtype, dst_rank, dst_shape, dst) ||
+        !tensorTypeOf(src_dtype, src_rank, src_shape, src))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_type_relation: bad shape");
+    if (assignable) *assignable = dst.assignableFrom(src) ? 1 : 0;
+    if (equal) *equal = dst.equals(src) ? 1 : 0;
+    return ok();
+}
 
 int camel_tensor_from_host(uint32_t dtype, int64_t rank, const int64_t *shape, const void *data,
                            uint64_t *handle) {
@@ -258,7 +304,7 @@ int camel_tensor_invoke(const char *uri, int64_t n_with, const camel_value *with
     std::vector<TypeCode> wc, nc;
     for (int64_t i = 0; i < n_with; ++i) wc.push_back(static_cast<TypeCode>(with[i].code));
     for (int64_t i = 0; i < n_norm; ++i) nc.push_back(static_cast<TypeCode>(norm[i].code));
-    std::optional<TypeCode> rtype;
+    std::optional<ResultType> rtype;
     const std::string full = "tensor:" + key;
     for (const auto &g : getTensorOperatorGroups()) {
         for (const auto &[guri, fn] : g.overloads) {
@@ -273,7 +319,7 @@ int camel_tensor_invoke(const char *uri, int64_t n_with, const camel_value *with
     return guarded([&] {
         Context ctx;
         const slot_t out = it->second(withView, normView, ctx);
-        result->code = static_cast<uint32_t>(*rtype);
+        result->code = static_cast<uint32_t>(rtype->code);
         result->slot = out;
         return ok();
     });
@@ -281,7 +327,7 @@ int camel_tensor_invoke(const char *uri, int64_t n_with, const camel_value *with
 
 int camel_tensor_resolve(const char *group, int64_t n_with, const uint32_t *with_codes,
                          int64_t n_norm, const uint32_t *norm_codes, char *uri, size_t cap,
-                         uint32_t *result_code) {
+                         uint32_t *result_code, uint32_t *result_elem) {
     if (!group || n_with < 0 || n_norm < 0 || (n_with > 0 && !with_codes) ||
         (n_norm > 0 && !norm_codes))
         return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_resolve: bad arguments");
@@ -298,7 +344,8 @@ int camel_tensor_resolve(const char *group, int64_t n_with, const uint32_t *with
                 std::memcpy(uri, r->first.data(), n);
                 uri[n] = '\0';
             }
-            if (result_code) *result_code = static_cast<uint32_t>(r->second);
+            if (result_code) *result_code = static_cast<uint32_t>(r->second.code);
+            if (result_elem) *result_elem = static_cast<uint32_t>(r->second.elem);
             return ok();
         }
     }

@@ -388,8 +388,9 @@ std::unordered_map<std::string, operator_t> getTensorOpsMap() {
 namespace {
 
 using Codes = std::vector<TypeCode>;
-using Result = std::optional<TypeCode>;
-constexpr TypeCode kTensor = TypeCode::Tensor;
+using Result = std::optional<ResultType>;
+// tensorType() (operators.cpp:41-43): Float32 unless an element type is given.
+const ResultType kTensor = tensorResult();
 
 // resolveTensorBinaryNamed (operators.cpp:111-124).
 Result binaryNamed(const Codes &, const Codes &n) {
@@ -406,7 +407,7 @@ Result compare(const Codes &, const Codes &n) {
     const bool la = n[0] == TypeCode::Array, ra = n[1] == TypeCode::Array;
     if ((l && r) || (l && isNumericScalar(n[1])) || (r && isNumericScalar(n[0])) ||
         (la && isNumericScalar(n[1])) || (isNumericScalar(n[0]) && ra))
-        return kTensor;
+        return tensorResult(TypeCode::Bool); // tensorType(Type::Bool()), operators.cpp:137
     return std::nullopt;
 }
 
@@ -477,13 +478,13 @@ const std::vector<OperatorGroup> &getTensorOperatorGroups() {
             {{"tensor:idx",
               [](const Codes &, const Codes &n) -> Result {
                   return n.size() == 2 && isTensor(n[0]) && n[1] == TypeCode::Int64
-                             ? Result(TypeCode::Float64)
+                             ? Result(scalarResult(TypeCode::Float64))
                              : std::nullopt;
               }},
              {"tensor:idx2d", [](const Codes &, const Codes &n) -> Result {
                   return n.size() == 3 && isTensor(n[0]) && n[1] == TypeCode::Int64 &&
                                  n[2] == TypeCode::Int64
-                             ? Result(TypeCode::Float64)
+                             ? Result(scalarResult(TypeCode::Float64))
                              : std::nullopt;
               }}}));
         for (auto [name, uri] : std::vector<std::pair<std::string, std::string>>{
@@ -509,26 +510,32 @@ const std::vector<OperatorGroup> &getTensorOperatorGroups() {
                                          if (n.empty() || n.size() > 3) return std::nullopt;
                                          for (TypeCode c : n)
                                              if (!isIntCode(c)) return std::nullopt;
-                                         return kTensor;
+                                         // tensorType(Type::Int64()), operators.cpp:382
+                                         return tensorResult(TypeCode::Int64);
                                      }}}));
         g.push_back(group("eye", {{"tensor:eye", [](const Codes &, const Codes &n) -> Result {
                                        return n.size() == 1 && isIntCode(n[0]) ? Result(kTensor)
                                                                                : std::nullopt;
                                    }}}));
         g.push_back(group("shape", {{"tensor:shape", [](const Codes &, const Codes &n) -> Result {
+                                         // intArrayType(), operators.cpp:45-48
                                          return n.size() == 1 && isTensor(n[0])
-                                                    ? Result(TypeCode::Array)
+                                                    ? Result(arrayResult(TypeCode::Int64))
                                                     : std::nullopt;
                                      }}}));
         g.push_back(group("sum", {{"tensor:sum",
                                    [](const Codes &, const Codes &n) -> Result {
                                        return n.size() == 1 && isTensor(n[0])
-                                                  ? Result(TypeCode::Float64)
+                                                  ? Result(scalarResult(TypeCode::Float64))
                                                   : std::nullopt;
                                    }},
                                   {"tensor:sum_axis", tensorAxis}}));
         g.push_back(group("max", {{"tensor:max_axis", tensorAxis}}));
-        g.push_back(group("argmax", {{"tensor:argmax_axis", tensorAxis}}));
+        // tensorType(Type::Int64()), operators.cpp:458
+        g.push_back(group("argmax", {{"tensor:argmax_axis", [](const Codes &w, const Codes &n) -> Result {
+                                          return tensorAxis(w, n) ? Result(tensorResult(TypeCode::Int64))
+                                                                  : std::nullopt;
+                                      }}}));
         for (auto [name, uri] : std::vector<std::pair<std::string, std::string>>{
                  {"exp", "tensor:exp"}, {"log", "tensor:log"}, {"transpose", "tensor:transpose"},
                  {"relu", "tensor:relu"}, {"softmax", "tensor:softmax"}})
@@ -550,7 +557,7 @@ const std::vector<OperatorGroup> &getTensorOperatorGroups() {
         g.push_back(group("show", {{"tensor:show", [](const Codes &, const Codes &n) -> Result {
                                         return n.size() == 1 &&
                                                        (isTensor(n[0]) || n[0] == TypeCode::Array)
-                                                   ? Result(TypeCode::Void)
+                                                   ? Result(scalarResult(TypeCode::Void))
                                                    : std::nullopt;
                                     }}}));
         g.push_back(group("dense", {{"tensor:dense", [](const Codes &w, const Codes &n) {

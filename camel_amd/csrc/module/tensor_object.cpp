@@ -20,7 +20,11 @@ void checkHip(int status) {
 }
 
 Storage::~Storage() {
-    if (dev) camel_hip_free(dev);
+    if (!dev) return;
+    // A destructor cannot report an error; a failed wait leaves the block
+    // out of the pool rather than risking its reuse under a live reader.
+    if (shared && camel_hip_device_sync() != 0) return;
+    camel_hip_free(dev);
 }
 
 namespace {

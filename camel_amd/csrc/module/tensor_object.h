@@ -49,6 +49,11 @@ struct Storage {
     std::unique_ptr<std::byte[]> host;
     bool devValid = false;
     bool hostValid = false;
+    // Set when the device block was handed out without a copy (DLPack
+    // export): a consumer may still read it on its own stream when the last
+    // reference goes, so the release waits for the whole device before the
+    // block returns to the pool, where the library stream could reuse it.
+    bool shared = false;
     std::mutex mutex; // residency transitions may race under a thread-pool scheduler
 };
 

@@ -72,7 +72,11 @@ KDL_CPU, KDL_ROCM = 1, 10
 
 _SIG = {
     "camel_tensor_last_error": ([], C.c_char_p),
-    "camel_tensor_abi_version": ([], C.c_int),
+    "camel_module_abi_version": ([], C.c_int),
+    "camel_tensor_type_string": ([_U32, _I64, C.POINTER(_I64), C.c_int, C.c_char_p, C.c_size_t,
+                                  C.POINTER(C.c_size_t)], C.c_int),
+    "camel_tensor_type_relation": ([_U32, _I64, C.POINTER(_I64), _U32, _I64, C.POINTER(_I64),
+                                    C.POINTER(C.c_int), C.POINTER(C.c_int)], C.c_int),
     "camel_tensor_from_host": ([_U32, _I64, C.POINTER(_I64), _P, C.POINTER(_U64)], C.c_int),
     "camel_tensor_to_host": ([_U64, _P, C.c_size_t], C.c_int),
     "camel_tensor_meta": ([_U64, C.POINTER(_U32), C.POINTER(_I64), C.POINTER(_I64), _I64], C.c_int),
@@ -89,7 +93,7 @@ _SIG = {
     "camel_tensor_invoke": ([C.c_char_p, _I64, C.POINTER(Value), _I64, C.POINTER(Value),
                              C.POINTER(Value)], C.c_int),
     "camel_tensor_resolve": ([C.c_char_p, _I64, C.POINTER(_U32), _I64, C.POINTER(_U32), C.c_char_p,
-                              C.c_size_t, C.POINTER(_U32)], C.c_int),
+                              C.c_size_t, C.POINTER(_U32), C.POINTER(_U32)], C.c_int),
     "camel_tensor_op_count": ([], _I64),
     "camel_tensor_op_name": ([_I64], C.c_char_p),
     "camel_tensor_group_count": ([], _I64),
@@ -249,9 +253,30 @@ class Tensor:
     @staticmethod
     def from_dlpack(obj) -> "Tensor":
         """A copy of a DLPack tensor (an object with __dlpack__, or a
-        "dltensor" capsule), from host memory or from this device.  A device
-        producer must have finished writing it (synchronise its stream)."""
-        cap = obj.__dlpack__() if hasattr(obj, "__dlpack__") else obj
+        "dltensor" capsule), from host memory or from this device.
+
+        For a device producer the copy is ordered after its pending writes:
+        the library stream is passed as the DLPack ``stream`` argument (the
+        producer makes that stream wait for its own), and a producer that
+        takes no stream argument is waited for with a whole-device
+        synchronisation.  A bare capsule must already be complete."""
+        from camel_amd import _hip
+        if hasattr(obj, "__dlpack__"):
+            on_device = (hasattr(obj, "__dlpack_device__")
+                         and int(obj.__dlpack_device__()[0]) == KDL_ROCM)
+            if on_device:
+                stream = _hip.load().camel_hip_stream()
+                if not stream:
+                    raise RuntimeError(_hip.load().camel_hip_last_error().decode())
+                try:
+                    cap = obj.__dlpack__(stream=int(stream))
+                except TypeError:
+                    cap = obj.__dlpack__()
+                    _hip.call("camel_hip_device_sync")
+            else:
+                cap = obj.__dlpack__()
+        else:
+            cap = obj
         managed = C.cast(_capsule_get(cap, b"dltensor"), C.POINTER(DLManagedTensor))
         h = _U64()
         _check(load().camel_tensor_from_dlpack(managed, C.byref(h)))
@@ -383,13 +408,44 @@ def call(uri: str, *norm, with_=()):
 
 def resolve(group: str, norm_codes, with_codes=()) -> tuple[str, int]:
     """Overload resolution of an operator group: (uri, result type code)."""
+    uri, code, _ = resolve_type(group, norm_codes, with_codes)
+    return uri, code
+
+
+def resolve_type(group: str, norm_codes, with_codes=()) -> tuple[str, int, int]:
+    """(uri, result type code, element type): the element type is a Tensor
+    result's dtype, an Array result's element type, else the code itself."""
     n = (_U32 * max(len(norm_codes), 1))(*norm_codes)
     w = (_U32 * max(len(with_codes), 1))(*with_codes)
     buf = C.create_string_buffer(128)
-    rc = _U32()
+    rc, re = _U32(), _U32()
     _check(load().camel_tensor_resolve(group.encode(), len(with_codes), w, len(norm_codes), n, buf,
-                                       128, C.byref(rc)))
-    return buf.value.decode(), rc.value
+                                       128, C.byref(rc), C.byref(re)))
+    return buf.value.decode(), rc.value, re.value
+
+
+def _shape_arg(shape):
+    shape = tuple(int(d) for d in shape)
+    return len(shape), (_I64 * max(len(shape), 1))(*shape)
+
+
+def tensor_type_string(dtype: int = TC_FLOAT32, shape=(), mangled: bool = False) -> str:
+    """TensorType::toString / mangle of Tensor<shape, dtype> (shape () = dynamic)."""
+    rank, dims = _shape_arg(shape)
+    need = C.c_size_t()
+    _check(load().camel_tensor_type_string(dtype, rank, dims, int(mangled), None, 0, C.byref(need)))
+    buf = C.create_string_buffer(need.value)
+    _check(load().camel_tensor_type_string(dtype, rank, dims, int(mangled), buf, need.value, None))
+    return buf.value.decode()
+
+
+def tensor_type_relation(dst, src) -> tuple[bool, bool]:
+    """(dst.assignableFrom(src), dst.equals(src)) for (dtype, shape) pairs."""
+    dr, dd = _shape_arg(dst[1])
+    sr, sd = _shape_arg(src[1])
+    a, e = C.c_int(), C.c_int()
+    _check(load().camel_tensor_type_relation(dst[0], dr, dd, src[0], sr, sd, C.byref(a), C.byref(e)))
+    return bool(a.value), bool(e.value)
 
 
 def op_names() -> list[str]:

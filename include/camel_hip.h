@@ -83,6 +83,11 @@ int camel_hip_current_device(int *device);
 const char *camel_hip_last_error(void);
 /* Blocks until all enqueued work is done. */
 int camel_hip_sync(void);
+/* Blocks until every stream of the library's device is idle, the library's
+ * and other libraries' alike (hipDeviceSynchronize): for payloads handed to
+ * consumers that read them on their own streams (zero-copy DLPack export).
+ * No reference counterpart (the reference is CPU-only). */
+int camel_hip_device_sync(void);
 /* The library's hipStream_t, as an opaque handle (for timing by callers). */
 void *camel_hip_stream(void);
 

@@ -119,10 +119,32 @@ int camel_array_release(uint64_t handle);
 int camel_tensor_invoke(const char *uri, int64_t n_with, const camel_value *with, int64_t n_norm,
                         const camel_value *norm, camel_value *result);
 /* Overload resolution of a group ("__mat__", "sum", "dense", ...): writes the
- * chosen URI and the result type code. */
+ * chosen URI, the result type code and the result's element type: the dtype
+ * of a Tensor result as the reference's resolvers give it (Float32 by default,
+ * modules/tensor/operators.cpp:41-43; Bool for the comparisons, 137; Int64
+ * for range and argmax, 382 and 458), the element type of an Array result
+ * (Int64 for shape, 45-48), and the result code itself otherwise.  Either
+ * output pointer may be NULL. */
 int camel_tensor_resolve(const char *group, int64_t n_with, const uint32_t *with_codes,
                          int64_t n_norm, const uint32_t *norm_codes, char *uri, size_t cap,
-                         uint32_t *result_code);
+                         uint32_t *result_code, uint32_t *result_elem);
+
+/* ---- TensorType (modules/tensor/type.h:32-59, type.cpp:21-145) ----------- */
+/* A tensor type is an element dtype (a CAMEL_TC_* primitive code) and a static
+ * shape of `rank` extents; rank 0 means dynamic (any shape), as an empty
+ * shape does in the reference. */
+/* TensorType::toString (mangled = 0, e.g. "Tensor", "Tensor<bool>",
+ * "Tensor<[2, 3], i64>"; type.cpp:64-81) or TensorType::mangle (mangled = 1,
+ * e.g. "T_;f32", "T2,3;i"; type.cpp:83-98), NUL-terminated into buf;
+ * *needed receives the size including the NUL. */
+int camel_tensor_type_string(uint32_t dtype, int64_t rank, const int64_t *shape, int mangled,
+                             char *buf, size_t cap, size_t *needed);
+/* TensorType::assignableFrom and equals (type.cpp:105-131): whether a value of
+ * type src may be assigned to dst (a Float32 dst takes any dtype; a dynamic
+ * shape on either side matches any shape), and whether the types are equal. */
+int camel_tensor_type_relation(uint32_t dst_dtype, int64_t dst_rank, const int64_t *dst_shape,
+                               uint32_t src_dtype, int64_t src_rank, const int64_t *src_shape,
+                               int *assignable, int *equal);
 /* Registered URI suffixes and group names. */
 int64_t camel_tensor_op_count(void);
 const char *camel_tensor_op_name(int64_t index);
@@ -154,8 +176,13 @@ int camel_chain_plan(uint64_t chain, int64_t rank, const int64_t *shape, char *b
                      size_t *needed);
 int camel_chain_release(uint64_t chain);
 
-/* Plugin ABI version the reference's loader checks (dynamic.h:29). */
-int camel_tensor_abi_version(void);
+/* The plugin ABI version the reference's module loader checks before it calls
+ * camel_module_create: CAMEL_MODULE_ABI_VERSION = 1
+ * (include/camel/core/module/dynamic.h:29,38; modules/camel_module_abi.cpp:22;
+ * checked in src/core/module/dynamic.cpp:118-178).  camel_module_create itself
+ * returns a C++ Module object of libcamel and belongs to the .cmo glue that
+ * is compiled against libcamel's headers (see the integration notes). */
+int camel_module_abi_version(void);
 
 #ifdef __cplusplus
 }

@@ -266,9 +266,11 @@ def conv2d_images(x, w, b, relu_: bool, n0: int, n1: int, stride: int = 1, pad: 
     return y[n0:n1]
 
 
-def maxpool2d(x: np.ndarray, k: int = 2, stride: int = 2) -> np.ndarray:
+def maxpool2d(x: np.ndarray, k: int = 2, stride: int = 2, kw: int | None = None) -> np.ndarray:
+    """Window k x kw (kw defaults to k), NCHW."""
+    kw = k if kw is None else kw
     N, Cc, H, W = x.shape
-    OH, OW = (H - k) // stride + 1, (W - k) // stride + 1
+    OH, OW = (H - k) // stride + 1, (W - kw) // stride + 1
     y = np.empty((N, Cc, OH, OW), dtype=np.float32)
-    _check(lib().ot_maxpool2d(ptr(np.ascontiguousarray(x)), ptr(y), N, Cc, H, W, k, k, stride))
+    _check(lib().ot_maxpool2d(ptr(np.ascontiguousarray(x)), ptr(y), N, Cc, H, W, k, kw, stride))
     return y

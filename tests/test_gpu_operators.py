@@ -217,3 +217,22 @@ def test_random_range_and_show(capfd):
     assert T.call("show", T.call("eye", 2)) is None
     out = capfd.readouterr().out
     assert out == "tensor([[      1.,       0.],\n        [      0.,       1.]], dtype=float32)\n"
+
+
+def test_operator_results_have_the_resolved_dtype():
+    # Each operator's result dtype at run time is the element type its group
+    # resolves (Tensor<bool> for compares, Tensor<i64> for range / argmax,
+    # Float32 otherwise; modules/tensor/operators.cpp:41-43, 137, 382, 458).
+    a = t(np.arange(6, dtype=np.float32).reshape(2, 3))
+    cases = [
+        ("__lt__", (a, 2.0), (T.TC_TENSOR, T.TC_FLOAT64)),
+        ("__eq__", (3.0, a), (T.TC_FLOAT64, T.TC_TENSOR)),
+        ("range", (5,), (T.TC_INT64,)),
+        ("argmax", (a, 1), (T.TC_TENSOR, T.TC_INT64)),
+        ("__add__", (a, a), (T.TC_TENSOR, T.TC_TENSOR)),
+        ("exp", (a,), (T.TC_TENSOR,)),
+    ]
+    for group, args, codes in cases:
+        uri, code, elem = T.resolve_type(group, list(codes))
+        out = T.call(uri, *args)
+        assert code == T.TC_TENSOR and out.dtype_code == elem, group

@@ -72,6 +72,13 @@ def test_hip_abi_rejects_extents_whose_products_overflow():
     assert lib.camel_hip_argmax_axis(H.DT_I64, None, 2**61, 2, 1, None) == H.ERR_SHAPE
     assert lib.camel_hip_softmax_rows(None, None, 2**62, 4) == H.ERR_SHAPE
     assert b"too large" in lib.camel_hip_last_error()
+    # The generic (Int64 / Bool) matmul: an extent past INT32_MAX is legal (the
+    # kernel indexes in int64), but byte counts that overflow are refused.
+    gm = lib.camel_hip_matmul_generic
+    assert gm(H.DT_I64, None, H.DT_I64, None, H.DT_I64, None, 2**31, 2**31, 2**31) == H.ERR_SHAPE
+    assert gm(H.DT_I64, None, H.DT_I64, None, H.DT_I64, None, 2**60, 1, 4) == H.ERR_SHAPE
+    assert gm(H.DT_BOOL, None, H.DT_BOOL, None, H.DT_BOOL, None, 4, 2**61, 1) == H.ERR_SHAPE
+    assert b"too large" in lib.camel_hip_last_error()
 
 
 def test_tensor_abi_exports_every_declared_symbol():
@@ -80,7 +87,9 @@ def test_tensor_abi_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert declared == set(T.exported_symbols())
-    assert lib.camel_tensor_abi_version() == 1
+    # The version the reference's loader checks (dynamic.h:29,38).
+    assert lib.camel_module_abi_version() == 1
+    assert not hasattr(lib, "camel_tensor_abi_version")
 
 
 def test_ops_map_keeps_reference_suffixes():
@@ -120,6 +129,78 @@ def test_groups_keep_reference_names():
 ])
 def test_resolution(group, norm, with_, uri, result):
     assert T.resolve(group, norm, with_) == (uri, result)
+
+
+F32, I64, BOOL, F64, VOID = T.TC_FLOAT32, T.TC_INT64, T.TC_BOOL, T.TC_FLOAT64, T.TC_VOID
+TEN, ARR = T.TC_TENSOR, T.TC_ARRAY
+
+
+@pytest.mark.parametrize("group,norm,with_,code,elem", [
+    # tensorType() = TensorType::Dynamic(Float32) by default (operators.cpp:41-43)
+    ("__add__", [TEN, TEN], [], TEN, F32),
+    ("__div__", [TEN, T.TC_INT32], [], TEN, F32),
+    ("__pow__", [TEN, F64], [], TEN, F32),
+    ("__mat__", [TEN, TEN], [], TEN, F32),
+    ("zeros", [ARR], [], TEN, F32),
+    ("full", [ARR, F64], [], TEN, F32),
+    ("eye", [I64], [], TEN, F32),
+    ("sum", [TEN, I64], [], TEN, F32),
+    ("max", [TEN, I64], [], TEN, F32),
+    ("exp", [TEN], [], TEN, F32),
+    ("transpose", [TEN], [], TEN, F32),
+    ("concat", [TEN, ARR, I64], [], TEN, F32),
+    ("reshape", [TEN, ARR], [], TEN, F32),
+    ("softmax", [TEN], [], TEN, F32),
+    ("dense", [TEN], [TEN, TEN], TEN, F32),
+    # comparisons: tensorType(Type::Bool()) (operators.cpp:137), every form
+    ("__lt__", [TEN, TEN], [], TEN, BOOL),
+    ("__le__", [TEN, F64], [], TEN, BOOL),
+    ("__gt__", [F32, TEN], [], TEN, BOOL),
+    ("__ge__", [ARR, I64], [], TEN, BOOL),
+    ("__eq__", [T.TC_INT32, ARR], [], TEN, BOOL),
+    # range and argmax: tensorType(Type::Int64()) (operators.cpp:382, 458)
+    ("range", [I64], [], TEN, I64),
+    ("range", [I64, I64, T.TC_INT32], [], TEN, I64),
+    ("argmax", [TEN, I64], [], TEN, I64),
+    # scalars, arrays and void keep their own codes
+    ("sum", [TEN], [], F64, F64),
+    ("__idx__", [TEN, I64], [], F64, F64),
+    ("shape", [TEN], [], ARR, I64),
+    ("show", [TEN], [], VOID, VOID),
+])
+def test_resolution_carries_the_reference_result_dtype(group, norm, with_, code, elem):
+    _, got_code, got_elem = T.resolve_type(group, norm, with_)
+    assert (got_code, got_elem) == (code, elem)
+
+
+@pytest.mark.parametrize("dtype,shape,text,mangled", [
+    (F32, (), "Tensor", "T_;f32"),
+    (BOOL, (), "Tensor<bool>", "T_;b"),
+    (I64, (), "Tensor<i64>", "T_;i"),
+    (F32, (2, 3), "Tensor<[2, 3]>", "T2,3;f32"),
+    (I64, (4,), "Tensor<[4], i64>", "T4;i"),
+    (F64, (1, 0, 5), "Tensor<[1, 0, 5], f64>", "T1,0,5;f"),
+])
+def test_tensor_type_strings(dtype, shape, text, mangled):
+    # TensorType::toString and mangle (modules/tensor/type.cpp:64-98)
+    assert T.tensor_type_string(dtype, shape) == text
+    assert T.tensor_type_string(dtype, shape, mangled=True) == mangled
+
+
+@pytest.mark.parametrize("dst,src,assignable,equal", [
+    ((F32, ()), (F32, ()), True, True),
+    ((F32, ()), (BOOL, (2, 2)), True, False),        # Float32 target takes any dtype / shape
+    ((BOOL, ()), (F32, ()), False, False),           # not the other way round
+    ((I64, ()), (I64, (7,)), True, False),           # dynamic target shape
+    ((I64, (7,)), (I64, ()), True, False),           # dynamic source shape
+    ((F32, (2, 3)), (F32, (3, 2)), False, False),    # static shapes must match
+    ((F32, (2, 3)), (I64, (2, 3)), True, False),
+    ((BOOL, (2, 3)), (BOOL, (2, 3)), True, True),
+    ((I64, (2,)), (BOOL, (2,)), False, False),
+])
+def test_tensor_type_assignability(dst, src, assignable, equal):
+    # TensorType::assignableFrom / equals (modules/tensor/type.cpp:105-131)
+    assert T.tensor_type_relation(dst, src) == (assignable, equal)
 
 
 @pytest.mark.parametrize("group,norm", [

@@ -155,6 +155,26 @@ def test_compare_matches_ieee(op, npop):
     assert np.array_equal(O.compare_scalar(op, a, 1.0), npop(a, F(1.0)).astype(np.uint8))
 
 
+@pytest.mark.parametrize("op,npop", [(O.LT, np.less), (O.LE, np.less_equal), (O.GT, np.greater),
+                                     (O.GE, np.greater_equal), (O.EQ, np.equal)])
+def test_compare_scalar_left_puts_the_scalar_first(op, npop):
+    # tensorCompareScalarLeft (runtime.cpp:848-861) computes s (op) t[i]; the
+    # ordered ops are not symmetric, so a swapped operand fails here.
+    a = SPECIALS
+    for s in SPECIALS:
+        want = npop(np.float64(s), a.astype(np.float64)).astype(np.uint8)
+        assert np.array_equal(O.compare_scalar(op, a, float(s), side=1), want), (op, s)
+    # The comparison runs in double: 0.1 (double) < fl32(0.1) = 0.10000000149...
+    # holds, while a float comparison of the two would be false.
+    t = np.array([0.1, -0.1, 2.0], F)
+    got = O.compare_scalar(op, t, 0.1, side=1)
+    assert np.array_equal(got, npop(0.1, t.astype(np.float64)).astype(np.uint8))
+    # Int64 tensor values go through double too (2^53 + 1 -> 2^53).
+    big = np.array([2 ** 53 + 1, -5], np.int64)
+    assert np.array_equal(O.compare_scalar(op, big, float(2 ** 53), side=1),
+                          npop(np.float64(2 ** 53), big.astype(np.float64)).astype(np.uint8))
+
+
 # --------------------------------------------------------------- relu (a7)
 
 def test_relu_idiom_sign_of_zero_nan_inf():
@@ -307,6 +327,43 @@ def test_maxpool_brute_force_and_ties():
     assert O.maxpool2d(n)[0, 0, 0, 0] == 3.0                 # NaN never replaces
     n0 = np.array([[[[np.nan, 5.0], [3.0, 2.0]]]], F)
     assert np.isnan(O.maxpool2d(n0)[0, 0, 0, 0])             # NaN as first element stays
+
+
+def _maxpool_brute(x, kh, kw, stride):
+    # Window (oh, ow) covers rows oh*stride .. +kh-1 and columns ow*stride ..
+    # +kw-1; its first element in row-major order is taken, then a later one
+    # replaces it only when strictly greater (tensorMaxAxis, runtime.cpp:953-958).
+    N, Cc, H, W = x.shape
+    OH, OW = (H - kh) // stride + 1, (W - kw) // stride + 1
+    y = np.empty((N, Cc, OH, OW), F)
+    for n in range(N):
+        for c in range(Cc):
+            for oh in range(OH):
+                for ow in range(OW):
+                    best = None
+                    for i in range(kh):
+                        for j in range(kw):
+                            v = float(x[n, c, oh * stride + i, ow * stride + j])
+                            if best is None or v > best:
+                                best = v
+                    y[n, c, oh, ow] = best
+    return y
+
+
+@pytest.mark.parametrize("kh,kw,stride", [(3, 3, 1), (2, 2, 1), (3, 3, 2), (2, 3, 2), (3, 2, 3),
+                                          (1, 1, 1)])
+def test_maxpool_general_windows_brute_force(kh, kw, stride):
+    # Small integers give many ties; -0.0 / +0.0 ties and NaNs check that the
+    # first element of the window wins a tie and that NaN never replaces.
+    rng = np.random.default_rng(kh * 100 + kw * 10 + stride)
+    x = rng.integers(-2, 3, size=(2, 3, 9, 11)).astype(F)
+    flat = x.reshape(-1)
+    flat[rng.choice(flat.size, 20, replace=False)] = -0.0
+    flat[rng.choice(flat.size, 6, replace=False)] = np.nan
+    got = O.maxpool2d(x, kh, stride, kw=kw)
+    want = _maxpool_brute(x, kh, kw, stride)
+    assert got.shape == want.shape
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 # ------------------------------------------------------- layout (a13)
