@@ -88,6 +88,8 @@ LayerChain *chainOf(uint64_t handle) {
 
 template <typename Fn> int guarded(Fn &&fn) {
     try {
+        // Objects made by a call that throws never reach the caller.
+        CreationScope scope;
         return fn();
     } catch (const RuntimeFault &e) {
         return fail(CAMEL_TENSOR_ERR_RUNTIME, e.what());

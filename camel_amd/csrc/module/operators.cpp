@@ -67,9 +67,11 @@ double scalarAsDouble(TypeCode code, ArgsView &args, size_t index) {
 slot_t wrap(TensorObject *t) { return toSlot(t); }
 
 // withTensorErrors (operators.cpp:103-109): any std::exception becomes a
-// RuntimeFault with the same text.
+// RuntimeFault with the same text.  Tensors the failed call made (its output,
+// temporaries of a composition) are released on the way out.
 template <typename Fn> slot_t withTensorErrors(Fn &&fn) {
     try {
+        CreationScope scope;
         return fn();
     } catch (const RuntimeFault &) {
         throw;

@@ -5,6 +5,7 @@
 #include "camel_hip.h"
 
 #include <cmath>
+#include <exception>
 #include <cstdio>
 #include <iomanip>
 #include <iostream>
@@ -570,13 +571,47 @@ Registry &registry() {
 } // namespace
 
 void registerObject(TensorObject *t) {
-    std::lock_guard<std::mutex> lock(registry().mutex);
-    registry().tensors.insert(t);
+    {
+        std::lock_guard<std::mutex> lock(registry().mutex);
+        registry().tensors.insert(t);
+    }
+    CreationScope::record(t);
 }
 
 void registerObject(ArrayObject *a) {
-    std::lock_guard<std::mutex> lock(registry().mutex);
-    registry().arrays.insert(a);
+    {
+        std::lock_guard<std::mutex> lock(registry().mutex);
+        registry().arrays.insert(a);
+    }
+    CreationScope::record(a);
+}
+
+namespace {
+thread_local CreationScope *t_scope = nullptr;
+} // namespace
+
+CreationScope::CreationScope() : parent_(t_scope), uncaught_(std::uncaught_exceptions()) {
+    t_scope = this;
+}
+
+CreationScope::~CreationScope() {
+    t_scope = parent_;
+    if (std::uncaught_exceptions() > uncaught_) {
+        // releaseTensor / releaseArray skip objects already released.
+        for (TensorObject *t : tensors_) releaseTensor(t);
+        for (ArrayObject *a : arrays_) releaseArray(a);
+    } else if (parent_) {
+        parent_->tensors_.insert(parent_->tensors_.end(), tensors_.begin(), tensors_.end());
+        parent_->arrays_.insert(parent_->arrays_.end(), arrays_.begin(), arrays_.end());
+    }
+}
+
+void CreationScope::record(TensorObject *t) {
+    if (t_scope) t_scope->tensors_.push_back(t);
+}
+
+void CreationScope::record(ArrayObject *a) {
+    if (t_scope) t_scope->arrays_.push_back(a);
 }
 
 bool releaseTensor(TensorObject *t) {

@@ -156,4 +156,30 @@ size_t liveTensorCount();
 // Releases every registered tensor and array; returns how many objects.
 size_t releaseAll();
 
+// Cleanup of an operator that throws: while a scope is active on a thread,
+// every tensor and array registered on that thread is recorded in it.  When
+// an exception leaves the scope, the recorded objects that are still live
+// are released (outputs and temporaries of the failed call, which the caller
+// never receives: the reference abandons its output when it throws).  When
+// the scope ends normally its records pass to the enclosing scope, so the
+// outputs of a nested operator are released too if the outer call fails
+// later.
+class CreationScope {
+  public:
+    CreationScope();
+    ~CreationScope();
+    CreationScope(const CreationScope &) = delete;
+    CreationScope &operator=(const CreationScope &) = delete;
+
+    // Records a new object in the innermost active scope of this thread.
+    static void record(TensorObject *t);
+    static void record(ArrayObject *a);
+
+  private:
+    CreationScope *parent_;
+    int uncaught_;
+    std::vector<TensorObject *> tensors_;
+    std::vector<ArrayObject *> arrays_;
+};
+
 } // namespace camel_amd::tensor

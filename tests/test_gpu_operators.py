@@ -236,3 +236,17 @@ def test_operator_results_have_the_resolved_dtype():
         uri, code, elem = T.resolve_type(group, list(codes))
         out = T.call(uri, *args)
         assert code == T.TC_TENSOR and out.dtype_code == elem, group
+
+
+def test_division_by_zero_releases_the_abandoned_output():
+    # The output is created on the device before the kernel's zero flag is
+    # read back; when the operator throws "Division by zero" that output is
+    # released, so a loop that catches the error does not grow memory.
+    a = t(np.ones((64, 64), np.float32))
+    z = t(np.zeros((64, 64), np.float32))
+    T.call("divide", a, a)  # uploads the operand
+    before = T.live_count()
+    for _ in range(3):
+        with pytest.raises(T.CamelError, match="Division by zero"):
+            T.call("divide", a, z)
+    assert T.live_count() == before

@@ -344,3 +344,15 @@ def test_release_bookkeeping():
     with pytest.raises(T.CamelError):
         a.handle = 12345
         a.release()
+
+
+def test_failed_operator_releases_what_it_made():
+    # concat(Array, Tensor) converts the array into a new host tensor
+    # (requireTensorOrConvertArray), then the shape check throws: the
+    # converted tensor never reaches the caller, so the layer releases it.
+    x = host(np.zeros((2, 3), np.float32))
+    arr = T.Array.from_list([[1.0, 2.0], [3.0, 4.0]])
+    before = T.live_count()
+    with pytest.raises(T.CamelError, match="concat requires equal non-axis dimensions"):
+        T.call("concat", arr, x, 0)
+    assert T.live_count() == before
