@@ -1,0 +1,335 @@
+"""Exact parity at the benchmark shapes: GEMM, dense and conv2d on small-integer
+operands, compared bit for bit over the whole output.
+
+Why this discriminates: with integer operands and biases, every product and
+every partial sum of a dot product is an integer; when
+``sum_k |A_ik| |B_kj| + |bias_j| < 2**24`` for an output (asserted for every
+output before a comparison), all of them are exact in fp32, whatever the
+summation order -- MFMA k-groups, LDS group sums, K splits, split reduces,
+column bands, thin-kernel quarters.  The reference's loop
+(modules/tensor/operators.cpp:757-766: fp64 accumulation in k order, then
+one rounding to fp32) yields the same exact integer, and so does numpy's
+float64 product, which these tests use as the reference at sizes the ijk
+oracle cannot finish in seconds (a row slab of the oracle is checked
+against it too).  A dropped, doubled or misplaced k term, tile, split or
+band moves some output by at least 1, so it fails here, where the general
+fp32 bound (1e-5 sqrt(K) sum |A||B|, about 0.66 per element at K = 4096)
+could not see it.
+
+Every kernel path of the GEMM and conv entry points is reached at its
+benchmark shape (the path each shape takes is named beside it).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from camel_amd import _hip as H
+from camel_amd import tensor as T
+from oracle import ffi as O
+from tests import hipkit as K
+
+pytestmark = pytest.mark.gpu
+
+P = C.c_void_p
+F = np.float32
+F64 = np.float64
+EXACT = 2.0 ** 24
+
+
+def ints(seed, shape, lo=-2, hi=2):
+    """Integers in [lo, hi] as fp32 (seeded)."""
+    return np.random.default_rng(seed).integers(lo, hi + 1, size=shape).astype(F)
+
+
+def relu32(y):
+    # x * (x > 0) in fp32: negatives become -0.0, as the reference idiom does
+    return y * (y > 0).astype(F)
+
+
+def exact_dense(a, b, bias=None, relu=False):
+    """A.B (+bias) (relu) in float64 (exact for these operands), rounded once."""
+    mag = np.abs(a).astype(F64) @ np.abs(b).astype(F64)
+    c = a.astype(F64) @ b.astype(F64)
+    if bias is not None:
+        mag += np.abs(bias).astype(F64)
+        c += bias.astype(F64)
+    assert mag.max(initial=0.0) < EXACT, "operands too large for exact fp32 partial sums"
+    y = c.astype(F)
+    return relu32(y) if relu else y
+
+
+def exact_conv(x, w, bias=None, stride=1, pad=0, relu=False):
+    """conv2d NCHW in float64, as a sum over (kh, kw) of channel contractions."""
+    N, Cin, H_, W_ = x.shape
+    Co, _, kh, kw = w.shape
+    OH, OW = (H_ + 2 * pad - kh) // stride + 1, (W_ + 2 * pad - kw) // stride + 1
+    xp = np.zeros((N, Cin, H_ + 2 * pad, W_ + 2 * pad), F64)
+    xp[:, :, pad:pad + H_, pad:pad + W_] = x
+    acc = np.zeros((Co, N, OH, OW), F64)
+    mag = np.zeros((Co, N, OH, OW), F64)
+    for i in range(kh):
+        for j in range(kw):
+            patch = xp[:, :, i:i + stride * (OH - 1) + 1:stride, j:j + stride * (OW - 1) + 1:stride]
+            wij = w[:, :, i, j].astype(F64)
+            acc += np.tensordot(wij, patch, axes=([1], [1]))
+            mag += np.tensordot(np.abs(wij), np.abs(patch), axes=([1], [1]))
+    acc = acc.transpose(1, 0, 2, 3)
+    mag = mag.transpose(1, 0, 2, 3)
+    if bias is not None:
+        acc = acc + bias.astype(F64)[None, :, None, None]
+        mag = mag + np.abs(bias).astype(F64)[None, :, None, None]
+    assert mag.max(initial=0.0) < EXACT, "operands too large for exact fp32 partial sums"
+    y = np.ascontiguousarray(acc).astype(F)
+    return relu32(y) if relu else y
+
+
+def pool2(y):
+    # the oracle's 2x2 / stride 2 pool: the window's first element, replaced
+    # only by a strictly greater one, so a -0.0 / +0.0 tie keeps the first
+    return O.maxpool2d(y, 2, 2)
+
+
+def assert_bits(got, want, what=""):
+    assert got.shape == want.shape, (got.shape, want.shape)
+    g, w = got.view(np.uint32), want.view(np.uint32)
+    bad = np.flatnonzero(g.reshape(-1) != w.reshape(-1))
+    assert bad.size == 0, (f"{what}: {bad.size} of {g.size} outputs differ; first at flat index "
+                           f"{bad[0]}: got {got.reshape(-1)[bad[0]]} want {want.reshape(-1)[bad[0]]}")
+
+
+def nchw4(a):
+    n, c, h, w = a.shape
+    return np.ascontiguousarray(a.reshape(n, c // 4, 4, h, w).transpose(0, 1, 3, 4, 2))
+
+
+def from_nchw4(a):
+    n, q, h, w, _ = a.shape
+    return np.ascontiguousarray(a.transpose(0, 1, 4, 2, 3).reshape(n, 4 * q, h, w))
+
+
+# --------------------------------------------------------------------- GEMM
+
+GEMM_SHAPES = [
+    # M, N, K, epilogue, path
+    (256, 256, 256, 0, "config 1: 32x32 tiles, four k-groups, K splits"),
+    (1024, 1024, 1024, 3, "64x64 tiles with two k-groups, one tile per CU"),
+    (1024, 1024, 784, 3, "MLP layer 1: 64x64 tiles, ragged first K stage"),
+    (2048, 2048, 2048, 0, "128x128 tiles, one round"),
+    (4096, 4096, 4096, 0, "headline: 8-wave 256x256 tiles, one round, XCD remap"),
+    (8192, 8192, 8192, 0, "256x256 tiles, four rounds"),
+    (4352, 4352, 512, 3, "256x256 whole round + K-split tail + ordered reduce"),
+    (512, 33024, 256, 3, "256x256 whole round + column band of small tiles"),
+    (512, 128, 9216, 3, "CNN dense1: 64x64 tiles, 16 K splits, XCD remap over splits"),
+    (200, 72, 1000, 1, "32x32 tiles with K splits"),
+    (2048, 2048, 1001, 0, "128x128 tiles, odd K: scalar A loads"),
+    (1000, 1003, 777, 3, "ragged M, N and K, scalar B loads"),
+    (16, 4096, 4096, 0, "skinny M = 16: streaming kernel, 4 chunks per work-group"),
+    (32, 4096, 4096, 3, "skinny M = 32: two 16-row groups"),
+    (8, 2048, 8192, 3, "skinny M < 16: rows past M read as zero"),
+    (16, 4094, 1000, 3, "skinny with N % 4 != 0: 32x128 MFMA tiles"),
+    (1024, 10, 1024, 3, "MLP layer 3: thin kernel, 16-wave rows, N <= 16"),
+    (512, 10, 128, 1, "CNN dense2: thin kernel"),
+    (2000, 32, 512, 3, "thin kernel, 16 < N <= 32"),
+]
+
+
+@pytest.mark.parametrize("M,N,Kd,epi,path", GEMM_SHAPES, ids=[s[4].split(":")[0] for s in GEMM_SHAPES])
+def test_sgemm_integer_operands_are_exact_at_full_size(M, N, Kd, epi, path):
+    print(f"exact sgemm {M}x{N}x{Kd} epi={epi} ({path})", flush=True)
+    seed = M * 131 + N * 7 + Kd
+    a, b = ints(seed, (M, Kd)), ints(seed + 1, (Kd, N))
+    bias = ints(seed + 2, (N,)) if epi & H.EPI_BIAS else None
+    want = exact_dense(a, b, bias, bool(epi & H.EPI_RELU))
+    got = K.sgemm(a, b, bias, epi)
+    assert_bits(got, want, path)
+    r = min(M, 4)
+    if r * N * Kd <= 3e8:
+        # the ijk oracle itself, on its first rows
+        ref = O.dense(a[:r], b, bias, bool(epi & H.EPI_RELU))
+        assert_bits(ref, want[:r], "oracle slab")
+
+
+def test_sgemm_exact_results_repeat_across_calls():
+    # Split partial scratch reused by a second, smaller call (skinny and tiles).
+    for M, N, Kd in ((16, 4096, 4096), (16, 1024, 8192), (512, 128, 9216), (200, 72, 1000)):
+        a, b = ints(M + Kd, (M, Kd)), ints(N + Kd, (Kd, N))
+        want = exact_dense(a, b)
+        assert_bits(K.sgemm(a, b), want, f"{M}x{N}x{Kd}")
+
+
+# ----------------------------------------------------------- fused dense paths
+
+def _dense_head(x, w1, b1, w2, b2, flags1, flags2, softmax):
+    M, K1 = x.shape
+    N1, N2 = w1.shape[1], w2.shape[1]
+    dx, dw1, db1, dw2, db2 = K.dev(x), K.dev(w1), K.dev(b1), K.dev(w2), K.dev(b2)
+    dy = K.empty(M * N2 * 4)
+    H.call("camel_hip_dense_head", P(dx.ptr), P(dw1.ptr), P(db1.ptr), P(dw2.ptr), P(db2.ptr),
+           P(dy.ptr), M, K1, N1, N2, flags1, flags2, softmax)
+    return K.host(dy, F, (M, N2))
+
+
+def softmax_close(got, logits):
+    p = O.softmax_rows(logits)
+    assert np.max(np.abs(got.astype(F64) - p) / np.maximum(p, 1e-30)) <= 1e-6
+
+
+def test_dense_head_on_split_partials_is_exact():
+    # The CNN head 512x9216 -> 128 (relu) -> 10: layer 2's thin kernel adds
+    # layer 1's 16 K-split partials itself.  The logits are exact; the fused
+    # softmax is within the softmax bar of the oracle's softmax of them.
+    x = ints(0x7000, (512, 9216), 0, 1)
+    w1, b1 = ints(0x7001, (9216, 128), -1, 1), ints(0x7002, (128,), -1, 1)
+    w2, b2 = ints(0x7003, (128, 10), -1, 1), ints(0x7004, (10,), -1, 1)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    h = exact_dense(x, w1, b1, True)
+    logits = exact_dense(h, w2, b2, False)
+    assert_bits(_dense_head(x, w1, b1, w2, b2, epi, H.EPI_BIAS, 0), logits, "head logits")
+    assert_bits(_dense_head(x, w1, b1, w2, b2, epi, epi, 0), relu32(logits), "head relu")
+    softmax_close(_dense_head(x, w1, b1, w2, b2, epi, H.EPI_BIAS, 1), logits)
+
+
+def test_dense_softmax_logits_are_exact_before_the_softmax():
+    # MLP layer 3 + softmax fused (1024 x 1024 -> 10): against the oracle's
+    # softmax of the exact logits.
+    x, w, b = ints(0x7010, (1024, 1024), 0, 2), ints(0x7011, (1024, 10)), ints(0x7012, (10,))
+    logits = exact_dense(x, w, b, False)
+    dx, dw, db = K.dev(x), K.dev(w), K.dev(b)
+    dy = K.empty(1024 * 10 * 4)
+    H.call("camel_hip_dense_softmax", P(dx.ptr), P(dw.ptr), P(db.ptr), P(dy.ptr), 1024, 10, 1024,
+           H.EPI_BIAS)
+    softmax_close(K.host(dy, F, (1024, 10)), logits)
+
+
+# ------------------------------------------------------------------- conv2d
+
+def _conv(x, w, b, geom, flags, pooled=False, x_layout=None, y_nchw4=False):
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    OH, OW = (H_ + 2 * pad - kh) // stride + 1, (W_ + 2 * pad - kw) // stride + 1
+    if pooled:
+        OH, OW = OH // 2, OW // 2
+    if x_layout == "nhwc":
+        x = np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+    elif x_layout == "nchw4":
+        x = nchw4(x)
+    dx, dw = K.dev(x), K.dev(w)
+    db = K.dev(b) if b is not None else None
+    dy = K.empty(N * Co * OH * OW * 4)
+    H.call("camel_hip_conv2d_pool2" if pooled else "camel_hip_conv2d", P(dx.ptr), P(dw.ptr),
+           P(db.ptr) if db else None, P(dy.ptr), N, Cin, H_, W_, Co, kh, kw, stride, pad, flags)
+    if y_nchw4:
+        return from_nchw4(K.host(dy, F, (N, Co // 4, OH, OW, 4)))
+    return K.host(dy, F, (N, Co, OH, OW))
+
+
+CONV_CASES = [
+    # geometry (N, C, H, W, Co, KH, KW, stride, pad), operand ranges, path
+    ((64, 64, 56, 56, 128, 3, 3, 1, 1), (-2, 2), "config 4: NCHW planes loader, column band"),
+    ((32, 64, 56, 56, 128, 3, 3, 1, 1), (-2, 2), "whole rounds + K-split tail"),
+    ((512, 1, 28, 28, 32, 3, 3, 1, 0), (-2, 2), "CNN conv1: direct kernel, K = 9"),
+    ((512, 32, 26, 26, 64, 3, 3, 1, 0), (-1, 1), "CNN conv2: planes loader, 64-row tiles"),
+    ((8, 12, 30, 30, 40, 3, 3, 1, 1), (-2, 2), "NCHW gather loader (C % 16 != 0)"),
+    ((16, 16, 33, 35, 130, 3, 3, 2, 1), (-2, 2), "16-channel stages, stride 2, Co > 128"),
+    ((4, 3, 40, 40, 16, 5, 5, 1, 2), (-2, 2), "gather loader, 5x5 window, pad 2"),
+    ((6, 2, 21, 19, 12, 4, 4, 1, 1), (-2, 2), "direct kernel, K = 32"),
+]
+
+
+@pytest.mark.parametrize("geom,rng_,path", CONV_CASES, ids=[c[2].split(":")[0] for c in CONV_CASES])
+def test_conv2d_integer_operands_are_exact_at_full_size(geom, rng_, path):
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    print(f"exact conv2d {geom} ({path})", flush=True)
+    seed = N * 1000 + Cin * 10 + Co
+    x = ints(seed, (N, Cin, H_, W_), *rng_)
+    w = ints(seed + 1, (Co, Cin, kh, kw), *rng_)
+    b = ints(seed + 2, (Co,), *rng_)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    want = exact_conv(x, w, b, stride, pad, relu=True)
+    assert_bits(_conv(x, w, b, geom, epi), want, path)
+    # the same values from the other addressing modes
+    if Cin % 4 == 0:
+        assert_bits(_conv(x, w, b, geom, epi | H.CONV_X_NHWC, x_layout="nhwc"), want, "x NHWC")
+        assert_bits(_conv(x, w, b, geom, epi | H.CONV_X_NCHW4, x_layout="nchw4"), want, "x NCHW4")
+    if Co % 4 == 0:
+        assert_bits(_conv(x, w, b, geom, epi | H.CONV_Y_NCHW4, y_nchw4=True), want, "y NCHW4")
+    wp = np.ascontiguousarray(w.transpose(0, 2, 3, 1))
+    assert_bits(_conv(x, wp, b, geom, epi | H.CONV_W_PACKED), want, "packed weights")
+    if want.shape[2] >= 2 and want.shape[3] >= 2:
+        assert_bits(_conv(x, w, b, geom, epi, pooled=True), pool2(want), "pooled")
+    if Co * want.shape[2] * want.shape[3] * Cin * kh * kw <= 3e8:
+        # the oracle's direct loop on image 0
+        ref = O.conv2d_images(x, w, b, True, 0, 1, stride, pad)
+        assert_bits(ref, want[:1], "oracle image 0")
+
+
+def test_cnn_pooled_conv2_from_nchw4_is_exact():
+    # The benchmarked CNN group: conv2 reads conv1's NCHW4 output in place
+    # with packed weights and stores only the 2x2 pooled values.
+    geom = (512, 32, 26, 26, 64, 3, 3, 1, 0)
+    x = ints(0x7100, (512, 32, 26, 26), 0, 2)
+    w = ints(0x7101, (64, 32, 3, 3), -1, 1)
+    b = ints(0x7102, (64,), -1, 1)
+    want = pool2(exact_conv(x, w, b, 1, 0, relu=True))
+    wp = np.ascontiguousarray(w.transpose(0, 2, 3, 1))
+    flags = H.EPI_BIAS | H.EPI_RELU | H.CONV_X_NCHW4 | H.CONV_W_PACKED
+    assert_bits(_conv(x, wp, b, geom, flags, pooled=True, x_layout="nchw4"), want, "pooled conv2")
+
+
+# ------------------------------------------------------------- layer chains
+
+@pytest.fixture
+def _release():
+    yield
+    T.release_all()
+
+
+def t(a):
+    return T.Tensor.from_numpy(np.asarray(a))
+
+
+def test_mlp_chain_full_batch_is_exact(_release):
+    # BASELINE config 2's shapes (1024 x 784 -> 1024 -> 1024 -> 10) through
+    # the fused chain: the logits exactly, then the softmax within its bar
+    # for every row.
+    dims = [784, 1024, 1024, 10]
+    x = ints(0x7200, (1024, 784), 0, 1)
+    wn = [ints(0x7201 + i, (dims[i], dims[i + 1]), -1, 1) for i in range(3)]
+    bn = [ints(0x7205 + i, (dims[i + 1],), -1, 1) for i in range(3)]
+    h = exact_dense(x, wn[0], bn[0], True)
+    h = exact_dense(h, wn[1], bn[1], True)
+    logits = exact_dense(h, wn[2], bn[2], False)
+    ws, bs = [t(w) for w in wn], [t(b) for b in bn]
+    head = T.Chain(("dense_relu", ws[0], bs[0]), ("dense_relu", ws[1], bs[1]), ("dense", ws[2], bs[2]))
+    assert_bits(head(t(x)).numpy(), logits, "MLP logits")
+    full = T.Chain(("dense_relu", ws[0], bs[0]), ("dense_relu", ws[1], bs[1]),
+                   ("dense", ws[2], bs[2]), "softmax")
+    softmax_close(full(t(x)).numpy(), logits)
+    head.release()
+    full.release()
+
+
+def test_cnn_chain_full_batch_is_exact(_release):
+    # BASELINE config 5's shapes at batch 512 through the fused chain (conv1
+    # direct -> NCHW4 -> pooled conv2 -> dense head on split partials): the
+    # logits exactly, then the softmax within its bar, for all 512 images.
+    x = ints(0x7300, (512, 1, 28, 28), 0, 1)
+    w1, b1 = ints(0x7301, (32, 1, 3, 3), -1, 1), ints(0x7302, (32,), -1, 1)
+    w2, b2 = ints(0x7303, (64, 32, 3, 3), -1, 1), ints(0x7304, (64,), -1, 1)
+    w3, b3 = ints(0x7305, (9216, 128), -1, 1), ints(0x7306, (128,), -1, 1)
+    w4, b4 = ints(0x7307, (128, 10), -1, 1), ints(0x7308, (10,), -1, 1)
+    h = exact_conv(x, w1, b1, relu=True)
+    h = pool2(exact_conv(h, w2, b2, relu=True)).reshape(512, 9216)
+    h = exact_dense(h, w3, b3, True)
+    logits = exact_dense(h, w4, b4, False)
+    tw = [t(a) for a in (w1, b1, w2, b2, w3, b3, w4, b4)]
+    layers = [("conv2d_relu", tw[0], tw[1]), ("conv2d_relu", tw[2], tw[3]), ("maxpool2d", 2, 2),
+              ("reshape", 512, 9216), ("dense_relu", tw[4], tw[5]), ("dense", tw[6], tw[7])]
+    head = T.Chain(*layers)
+    assert head.plan((512, 1, 28, 28))[:2] == ["conv2d_relu y=nchw4",
+                                               "conv2d_relu+maxpool2d(2,2) x=nchw4"]
+    assert_bits(head(t(x)).numpy(), logits, "CNN logits")
+    full = T.Chain(*layers, "softmax")
+    softmax_close(full(t(x)).numpy(), logits)
+    head.release()
+    full.release()
