@@ -62,6 +62,7 @@ _SIGNATURES = {
     "camel_hip_eye": [_P, _I64],
     "camel_hip_arange": [_P, _I64, _I64, _I64],
     "camel_hip_sgemm": [_P, _P, _P, _I64, _I64, _I64, _P, _I],
+    "camel_hip_sgemm_noalloc": [_P, _P, _P, _I64, _I64, _I64, _P, _I],
     "camel_hip_matmul_generic": [_I, _P, _I, _P, _I, _P, _I64, _I64, _I64],
     "camel_hip_conv2d": [_P, _P, _P, _P] + [_I64] * 9 + [_I],
     "camel_hip_conv2d_pool2": [_P, _P, _P, _P] + [_I64] * 9 + [_I],

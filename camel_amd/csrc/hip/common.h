@@ -28,8 +28,16 @@ int check_launch(const char *kernel);
 
 // Lazily initialises device 0; returns a status.
 int ensure_init();
+// True once a device has been initialised (no initialisation is attempted).
+bool initialised();
 hipStream_t stream();
 int device_cu_count();
+
+// The allocation-free entry points' scratch: the device address of the
+// library's static scratch array on the current device (CAMEL_HIP_NOALLOC_
+// SCRATCH_BYTES long, 256-byte aligned), looked up once per device at
+// initialisation; nullptr before that.
+float *noalloc_scratch();
 
 // Device error flag: cleared by a fill kernel before a checked launch and read
 // back (synchronously) after it.

@@ -1669,22 +1669,51 @@ template <class T> int64_t tiles_of(int64_t M, int64_t N) {
     return ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
 }
 
-// Scratch for split-K partials, grown on demand (kept for the process).
+// Scratch for split-K partials: a pool block grown on demand (kept for the
+// process), or, while an allocation-free call runs, the library's static
+// scratch (FixedPartials).  Callers hold the library lock throughout.
 float *g_partial = nullptr;
 size_t g_partial_bytes = 0;
+float *g_fixed_partial = nullptr; // non-null only inside an allocation-free call
+size_t g_fixed_partial_bytes = 0;
 
-int ensure_partial(size_t bytes) {
-    if (bytes <= g_partial_bytes) return CAMEL_HIP_OK;
-    if (g_partial) {
-        CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
-        camel_hip_free(g_partial);
-        g_partial = nullptr;
-        g_partial_bytes = 0;
+// Routes the partial sums of the calls made in its lifetime to a caller-
+// provided buffer of `bytes` (the static scratch); nothing is allocated.
+struct FixedPartials {
+    FixedPartials(float *p, size_t bytes) {
+        g_fixed_partial = p;
+        g_fixed_partial_bytes = bytes;
     }
-    void *p = nullptr;
-    CAMEL_RETURN_IF(camel_hip_malloc(&p, bytes));
-    g_partial = static_cast<float *>(p);
-    g_partial_bytes = bytes;
+    ~FixedPartials() {
+        g_fixed_partial = nullptr;
+        g_fixed_partial_bytes = 0;
+    }
+    FixedPartials(const FixedPartials &) = delete;
+    FixedPartials &operator=(const FixedPartials &) = delete;
+};
+
+// A buffer of at least `bytes` for split-K partials, into *out.
+int partial_buffer(size_t bytes, float **out) {
+    if (g_fixed_partial) {
+        // The allocation-free entry points check their need up front.
+        if (bytes > g_fixed_partial_bytes)
+            return fail(CAMEL_HIP_ERR_SHAPE, "split-K partials exceed the static scratch");
+        *out = g_fixed_partial;
+        return CAMEL_HIP_OK;
+    }
+    if (bytes > g_partial_bytes) {
+        if (g_partial) {
+            CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
+            camel_hip_free(g_partial);
+            g_partial = nullptr;
+            g_partial_bytes = 0;
+        }
+        void *p = nullptr;
+        CAMEL_RETURN_IF(camel_hip_malloc(&p, bytes));
+        g_partial = static_cast<float *>(p);
+        g_partial_bytes = bytes;
+    }
+    *out = g_partial;
     return CAMEL_HIP_OK;
 }
 
@@ -1694,31 +1723,49 @@ bool skinny_eligible(int64_t M, int64_t N, int64_t K, const float *B, const floa
            ((uintptr_t)C & 15) == 0 && (K + SK_CHUNK - 1) / SK_CHUNK <= SK_MAX_KGROUPS;
 }
 
-int launch_skinny(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
-                  int flags) {
-    const int strips = (N + SK_COLS - 1) / SK_COLS;
+// Shape of a skinny launch: chunks per work-group (ch) and work-groups along
+// K (nks; their partials need nks * M * N floats when nks > 1).
+struct SkinnyPlan {
+    int ch, nks;
+};
+
+SkinnyPlan plan_skinny(int64_t N, int64_t K) {
+    const int64_t strips = (N + SK_COLS - 1) / SK_COLS;
     // Chunks per work-group: the most that still leaves one work-group per
     // CU (fewer, longer streams measured faster than more, shorter ones).
     const int cus = std::max(1, device_cu_count());
     int ch = 1;
     for (int c : {4, 2}) {
-        if ((int64_t)strips * ((K + SK_CHUNK * c - 1) / (SK_CHUNK * c)) >= cus) {
+        if (strips * ((K + SK_CHUNK * c - 1) / (SK_CHUNK * c)) >= cus) {
             ch = c;
             break;
         }
     }
+    return {ch, (int)((K + SK_CHUNK * ch - 1) / (SK_CHUNK * ch))};
+}
+
+size_t skinny_partial_bytes(int64_t M, int64_t N, int64_t K) {
+    const SkinnyPlan p = plan_skinny(N, K);
+    return p.nks > 1 ? (size_t)p.nks * M * N * sizeof(float) : 0;
+}
+
+int launch_skinny(const float *A, const float *B, float *C, int M, int N, int K, const float *bias,
+                  int flags) {
+    const int strips = (N + SK_COLS - 1) / SK_COLS;
+    const int ch = plan_skinny(N, K).ch;
     const int mt = M <= 16 ? 1 : 2;
     const int a_vec = M >= 16 * mt && K % 4 == 0 && ((uintptr_t)A & 15) == 0;
     auto go = [&](auto kernel, int chunks) -> int {
         const int nks = (K + SK_CHUNK * chunks - 1) / (SK_CHUNK * chunks);
-        if (nks > 1) CAMEL_RETURN_IF(ensure_partial((size_t)nks * M * N * sizeof(float)));
+        float *partial = nullptr;
+        if (nks > 1) CAMEL_RETURN_IF(partial_buffer((size_t)nks * M * N * sizeof(float), &partial));
         hipLaunchKernelGGL(kernel, dim3((unsigned)strips, (unsigned)nks), dim3(SK_WAVES * 64), 0,
-                           stream(), A, B, C, M, N, K, bias, flags, g_partial, a_vec);
+                           stream(), A, B, C, M, N, K, bias, flags, partial, a_vec);
         CAMEL_RETURN_IF(check_launch("sgemm_skinny_kernel"));
         if (nks == 1) return CAMEL_HIP_OK;
         const int64_t total4 = (int64_t)M * N / 4;
         hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((total4 + 255) / 256)), dim3(256),
-                           0, stream(), reinterpret_cast<const float4 *>(g_partial),
+                           0, stream(), reinterpret_cast<const float4 *>(partial),
                            reinterpret_cast<float4 *>(C), M, N, nks, bias, flags);
         return check_launch("skinny_reduce_kernel");
     };
@@ -1746,30 +1793,45 @@ template <class T, int AMODE, int BMODE> int resident_slots() {
     return slots;
 }
 
-// Runs tiles [tile_begin, tile_begin + ntiles) with `splits` K splits; split
-// launches write partials that tile_reduce_kernel folds into C.  With
-// `partials_only` the reduce is left to the caller: the partials stay in
-// g_partial and *partials_only receives the split count they hold.
-template <class T, int AMODE, int BMODE>
-int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char *name,
-                 int *partials_only = nullptr) {
-    g.tile_begin = tile_begin;
-    const int stages = (g.K + T::BK - 1) / T::BK;
+// K range per split and the split count a launch really runs for a request
+// of `splits`: whole BK stages per split, no empty split.
+template <class T> void split_k(int K, int splits, int &k_per_split, int &used) {
+    const int stages = (K + T::BK - 1) / T::BK;
     splits = std::max(1, std::min(splits, stages));
     const int kps_stages = (stages + splits - 1) / splits;
-    g.k_per_split = std::max(1, kps_stages) * T::BK;
-    splits = std::max(1, (g.K + g.k_per_split - 1) / g.k_per_split);
+    k_per_split = std::max(1, kps_stages) * T::BK;
+    used = std::max(1, (K + k_per_split - 1) / k_per_split);
+}
+
+// Partial-sum bytes of a launch of `ntiles` tiles asked to split K `splits`
+// ways (0 when it runs unsplit and is not a partials-only launch).
+template <class T> size_t range_partial_bytes(int K, int ntiles, int splits, bool partials_only) {
+    int kps = 0, used = 1;
+    split_k<T>(K, splits, kps, used);
+    if (used <= 1 && !partials_only) return 0;
+    return (size_t)used * ntiles * T::BM * T::BN * sizeof(float);
+}
+
+// Runs tiles [tile_begin, tile_begin + ntiles) with `splits` K splits; split
+// launches write partials that tile_reduce_kernel folds into C.  With
+// `partials_only` the reduce is left to the caller: *partials_only receives
+// the split count and *partials_at the buffer the partials stay in.
+template <class T, int AMODE, int BMODE>
+int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char *name,
+                 int *partials_only = nullptr, float **partials_at = nullptr) {
+    g.tile_begin = tile_begin;
+    split_k<T>(g.K, splits, g.k_per_split, splits);
     g.partial = nullptr;
     if (splits > 1 || partials_only) { // a partials-only launch writes partials even unsplit
-        CAMEL_RETURN_IF(
-            ensure_partial((size_t)splits * ntiles * T::BM * T::BN * sizeof(float)));
-        g.partial = g_partial;
+        CAMEL_RETURN_IF(partial_buffer(
+            (size_t)splits * ntiles * T::BM * T::BN * sizeof(float), &g.partial));
     }
     hipLaunchKernelGGL((sgemm_kernel<T, AMODE, BMODE>), dim3((unsigned)ntiles, (unsigned)splits),
                        dim3(T::THREADS), 0, stream(), g);
     CAMEL_RETURN_IF(check_launch(name));
     if (partials_only) {
         *partials_only = splits;
+        if (partials_at) *partials_at = g.partial;
         return CAMEL_HIP_OK;
     }
     if (splits > 1) {
@@ -1807,27 +1869,60 @@ using BandTile = Tile<64, (T::BK >= 32 ? 32 : 64), T::BK, 2, (T::BK >= 32 ? 1 : 
 //     -> 128 3x3 conv,
 //     whose 1568 tiles leave 32 after 3 rounds);
 //   * otherwise the leftover tiles are split along K and reduced in order.
-template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, const char *name) {
+// The launches run_gemm makes: tiles [0, head) unsplit (or all tiles with
+// `head_splits` when the caller split every tile), then either nothing, a
+// column band of small tiles from column band_n, or tiles [head, head + tail)
+// with tail_splits K splits.
+struct GemmSchedule {
+    int head = 0, head_splits = 1;
+    bool band = false;
+    int band_n = 0;
+    int tail = 0, tail_splits = 1;
+};
+
+template <class T, int AMODE, int BMODE> GemmSchedule schedule_gemm(const GemmArgs &g, int splits) {
+    GemmSchedule s;
     const int tiles_m = (g.M + T::BM - 1) / T::BM;
     const int tiles = (int)((int64_t)tiles_m * ((g.N + T::BN - 1) / T::BN));
-    if (splits > 1) return launch_range<T, AMODE, BMODE>(g, 0, tiles, splits, name);
+    s.head = tiles;
+    if (splits > 1) {
+        s.head_splits = splits;
+        return s;
+    }
     const int slots = resident_slots<T, AMODE, BMODE>();
     const int stages = (g.K + T::BK - 1) / T::BK;
     const int full = tiles / slots, rem = tiles % slots;
-    if (full == 0 || rem == 0 || stages < 4 || rem * 4 > slots)
-        return launch_range<T, AMODE, BMODE>(g, 0, tiles, 1, name);
-    const int dp = full * slots;
-    CAMEL_RETURN_IF((launch_range<T, AMODE, BMODE>(g, 0, dp, 1, name)));
+    if (full == 0 || rem == 0 || stages < 4 || rem * 4 > slots) return s;
+    s.head = full * slots;
     if (tiles_m <= GROUP_M && rem % tiles_m == 0) {
+        s.band = true;
+        s.band_n = s.head / tiles_m * T::BN;
+        return s;
+    }
+    s.tail = rem;
+    s.tail_splits = std::max(1, std::min(slots / rem, stages / 2));
+    return s;
+}
+
+// Partial-sum bytes the schedule needs (the band runs unsplit).
+template <class T> size_t schedule_partial_bytes(const GemmArgs &g, const GemmSchedule &s) {
+    return std::max(range_partial_bytes<T>(g.K, s.head, s.head_splits, false),
+                    s.tail ? range_partial_bytes<T>(g.K, s.tail, s.tail_splits, false) : 0);
+}
+
+template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, const char *name) {
+    const GemmSchedule s = schedule_gemm<T, AMODE, BMODE>(g, splits);
+    CAMEL_RETURN_IF((launch_range<T, AMODE, BMODE>(g, 0, s.head, s.head_splits, name)));
+    if (s.band) {
         using TB = BandTile<T>;
         GemmArgs band = g;
-        band.n_begin = dp / tiles_m * T::BN;
+        band.n_begin = s.band_n;
         const int band_tiles =
             (int)((int64_t)((g.M + TB::BM - 1) / TB::BM) * ((g.N - band.n_begin + TB::BN - 1) / TB::BN));
         return launch_range<TB, AMODE, BMODE>(band, 0, band_tiles, 1, name);
     }
-    const int tail_splits = std::max(1, std::min(slots / rem, stages / 2));
-    return launch_range<T, AMODE, BMODE>(g, dp, rem, tail_splits, name);
+    if (s.tail) return launch_range<T, AMODE, BMODE>(g, s.head, s.tail, s.tail_splits, name);
+    return CAMEL_HIP_OK;
 }
 
 template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool bvec) {
@@ -1835,6 +1930,20 @@ template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool
     if (avec) return run_gemm<T, LOAD_VEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
     if (bvec) return run_gemm<T, LOAD_SCALAR, LOAD_VEC>(g, splits, "sgemm_kernel");
     return run_gemm<T, LOAD_SCALAR, LOAD_SCALAR>(g, splits, "sgemm_kernel");
+}
+
+// Partial-sum bytes launch_gemm_modes<T> will need for these arguments.
+template <class T> size_t gemm_modes_partial_bytes(const GemmArgs &g, int splits, bool avec, bool bvec) {
+    GemmSchedule s;
+    if (avec && bvec)
+        s = schedule_gemm<T, LOAD_VEC, LOAD_VEC>(g, splits);
+    else if (avec)
+        s = schedule_gemm<T, LOAD_VEC, LOAD_SCALAR>(g, splits);
+    else if (bvec)
+        s = schedule_gemm<T, LOAD_SCALAR, LOAD_VEC>(g, splits);
+    else
+        s = schedule_gemm<T, LOAD_SCALAR, LOAD_SCALAR>(g, splits);
+    return schedule_partial_bytes<T>(g, s);
 }
 
 // The split-K launch run_gemm makes for `splits` > 1, without its reduce:
@@ -1845,15 +1954,16 @@ int launch_split_partials(GemmArgs g, int splits, bool avec, bool bvec, SplitPar
     const int tiles_m = (g.M + T::BM - 1) / T::BM, tiles_n = (g.N + T::BN - 1) / T::BN;
     const int tiles = tiles_m * tiles_n;
     int used = 0;
+    float *at = nullptr;
     if (avec && bvec)
-        CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_VEC>(g, 0, tiles, splits, "sgemm_kernel", &used)));
+        CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_VEC>(g, 0, tiles, splits, "sgemm_kernel", &used, &at)));
     else if (avec)
-        CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_SCALAR>(g, 0, tiles, splits, "sgemm_kernel", &used)));
+        CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_SCALAR>(g, 0, tiles, splits, "sgemm_kernel", &used, &at)));
     else if (bvec)
-        CAMEL_RETURN_IF((launch_range<T, LOAD_SCALAR, LOAD_VEC>(g, 0, tiles, splits, "sgemm_kernel", &used)));
+        CAMEL_RETURN_IF((launch_range<T, LOAD_SCALAR, LOAD_VEC>(g, 0, tiles, splits, "sgemm_kernel", &used, &at)));
     else
-        CAMEL_RETURN_IF((launch_range<T, LOAD_SCALAR, LOAD_SCALAR>(g, 0, tiles, splits, "sgemm_kernel", &used)));
-    out.partial = g_partial;
+        CAMEL_RETURN_IF((launch_range<T, LOAD_SCALAR, LOAD_SCALAR>(g, 0, tiles, splits, "sgemm_kernel", &used, &at)));
+    out.partial = at;
     out.bias = g.bias;
     out.flags = g.flags;
     out.splits = used;
@@ -2281,23 +2391,21 @@ int conv2d_run(const float *x, const float *w, const float *bias, float *y, int6
     return CAMEL_HIP_OK;
 }
 
-} // namespace
-} // namespace camel_hip
-
-using namespace camel_hip;
-
-extern "C" {
-
-int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
-                    const float *bias, int flags) {
-    if (M < 0 || N < 0 || K < 0) return fail(CAMEL_HIP_ERR_SHAPE, "sgemm: negative dimension");
+// Argument checks of the sgemm entry points (before any device work).
+int sgemm_check(const float *A, const float *B, const float *C, int64_t M, int64_t N, int64_t K,
+                const float *bias, int flags, const char *name) {
+    const std::string who(name);
+    if (M < 0 || N < 0 || K < 0) return fail(CAMEL_HIP_ERR_SHAPE, who + ": negative dimension");
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
-        return fail(CAMEL_HIP_ERR_SHAPE, "sgemm: dimension too large");
-    if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, "sgemm: null bias");
-    if (M == 0 || N == 0) return ok();
-    if (!C || (K > 0 && (!A || !B))) return fail(CAMEL_HIP_ERR_ARG, "sgemm: null operand");
-    CAMEL_LOCK();
-    CAMEL_INIT_OR_RETURN();
+        return fail(CAMEL_HIP_ERR_SHAPE, who + ": dimension too large");
+    if ((flags & CAMEL_EPI_BIAS) && !bias) return fail(CAMEL_HIP_ERR_ARG, who + ": null bias");
+    if (M == 0 || N == 0) return CAMEL_HIP_OK;
+    if (!C || (K > 0 && (!A || !B))) return fail(CAMEL_HIP_ERR_ARG, who + ": null operand");
+    return CAMEL_HIP_OK;
+}
+
+GemmArgs sgemm_args(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
+                    const float *bias, int flags) {
     GemmArgs g{};
     g.A = A;
     g.B = B;
@@ -2310,38 +2418,116 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
     g.ldb = (int)N;
     g.ldc = (int)N;
     g.flags = flags;
-    if (thin_eligible(M, N, K)) {
-        CAMEL_RETURN_IF(launch_thin(A, B, C, (int)M, (int)N, (int)K, bias, flags));
-        return ok();
-    }
-    if (skinny_eligible(M, N, K, B, C)) {
-        CAMEL_RETURN_IF(launch_skinny(A, B, C, (int)M, (int)N, (int)K, bias, flags));
-        return ok();
-    }
-    const bool avec = (K % 4 == 0) && ((uintptr_t)A % 16 == 0);
-    const bool bvec = (N % 4 == 0) && ((uintptr_t)B % 16 == 0);
+    return g;
+}
+
+// The kernels camel_hip_sgemm runs for a problem, and the bytes of split-K
+// partial sums they need (0 when nothing is split).
+enum class SgemmPath { Thin, Skinny, Tiles };
+struct SgemmPlan {
+    SgemmPath path;
     Cfg cfg;
-    int splits, bk;
-    choose(M, N, K, device_cu_count(), cfg, splits, bk);
-    int rc;
-    switch (cfg) {
+    int splits;
+    bool avec, bvec;
+    size_t partial_bytes;
+};
+
+SgemmPlan plan_sgemm(const GemmArgs &g) {
+    SgemmPlan p{SgemmPath::Tiles, Cfg::Big, 1, false, false, 0};
+    if (thin_eligible(g.M, g.N, g.K)) {
+        p.path = SgemmPath::Thin;
+        return p;
+    }
+    if (skinny_eligible(g.M, g.N, g.K, g.B, g.C)) {
+        p.path = SgemmPath::Skinny;
+        p.partial_bytes = skinny_partial_bytes(g.M, g.N, g.K);
+        return p;
+    }
+    p.avec = (g.K % 4 == 0) && ((uintptr_t)g.A % 16 == 0);
+    p.bvec = (g.N % 4 == 0) && ((uintptr_t)g.B % 16 == 0);
+    int bk = 0;
+    choose(g.M, g.N, g.K, device_cu_count(), p.cfg, p.splits, bk);
+    switch (p.cfg) {
     case Cfg::Big:
-        rc = launch_gemm_modes<TileBig>(g, splits, avec, bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileBig>(g, p.splits, p.avec, p.bvec);
         break;
     case Cfg::Mid:
-        rc = launch_gemm_modes<TileMid>(g, splits, avec, bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileMid>(g, p.splits, p.avec, p.bvec);
         break;
     case Cfg::Tiny:
-        rc = launch_gemm_modes<TileTiny>(g, splits, avec, bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileTiny>(g, p.splits, p.avec, p.bvec);
         break;
     case Cfg::Small:
-        rc = launch_gemm_modes<TileSmall>(g, splits, avec, bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileSmall>(g, p.splits, p.avec, p.bvec);
         break;
     default:
-        rc = launch_gemm_modes<TileSkinny>(g, splits, avec, bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileSkinny>(g, p.splits, p.avec, p.bvec);
         break;
     }
-    CAMEL_RETURN_IF(rc);
+    return p;
+}
+
+int run_sgemm(const GemmArgs &g, const SgemmPlan &p) {
+    switch (p.path) {
+    case SgemmPath::Thin:
+        return launch_thin(g.A, g.B, g.C, g.M, g.N, g.K, g.bias, g.flags);
+    case SgemmPath::Skinny:
+        return launch_skinny(g.A, g.B, g.C, g.M, g.N, g.K, g.bias, g.flags);
+    default:
+        break;
+    }
+    switch (p.cfg) {
+    case Cfg::Big:
+        return launch_gemm_modes<TileBig>(g, p.splits, p.avec, p.bvec);
+    case Cfg::Mid:
+        return launch_gemm_modes<TileMid>(g, p.splits, p.avec, p.bvec);
+    case Cfg::Tiny:
+        return launch_gemm_modes<TileTiny>(g, p.splits, p.avec, p.bvec);
+    case Cfg::Small:
+        return launch_gemm_modes<TileSmall>(g, p.splits, p.avec, p.bvec);
+    default:
+        return launch_gemm_modes<TileSkinny>(g, p.splits, p.avec, p.bvec);
+    }
+}
+
+} // namespace
+} // namespace camel_hip
+
+using namespace camel_hip;
+
+extern "C" {
+
+int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
+                    const float *bias, int flags) {
+    CAMEL_RETURN_IF(sgemm_check(A, B, C, M, N, K, bias, flags, "sgemm"));
+    if (M == 0 || N == 0) return ok();
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    const GemmArgs g = sgemm_args(A, B, C, M, N, K, bias, flags);
+    CAMEL_RETURN_IF(run_sgemm(g, plan_sgemm(g)));
+    return ok();
+}
+
+int camel_hip_sgemm_noalloc(const float *A, const float *B, float *C, int64_t M, int64_t N,
+                            int64_t K, const float *bias, int flags) {
+    CAMEL_RETURN_IF(sgemm_check(A, B, C, M, N, K, bias, flags, "sgemm_noalloc"));
+    if (M == 0 || N == 0) return ok();
+    CAMEL_LOCK();
+    // Initialisation allocates (stream, error flag): it belongs to set-up.
+    if (!initialised())
+        return fail(CAMEL_HIP_ERR_ARG, "sgemm_noalloc: call camel_hip_init before this entry point");
+    float *scratch = noalloc_scratch();
+    if (!scratch) return fail(CAMEL_HIP_ERR_RUNTIME, "sgemm_noalloc: static scratch not set up");
+    const GemmArgs g = sgemm_args(A, B, C, M, N, K, bias, flags);
+    const SgemmPlan plan = plan_sgemm(g);
+    if (plan.partial_bytes > CAMEL_HIP_NOALLOC_SCRATCH_BYTES)
+        return fail(CAMEL_HIP_ERR_SHAPE,
+                    "sgemm_noalloc: this shape needs " + std::to_string(plan.partial_bytes) +
+                        " bytes of split-K scratch, more than the " +
+                        std::to_string((size_t)CAMEL_HIP_NOALLOC_SCRATCH_BYTES) +
+                        "-byte static scratch");
+    FixedPartials fixed(scratch, CAMEL_HIP_NOALLOC_SCRATCH_BYTES);
+    CAMEL_RETURN_IF(run_sgemm(g, plan));
     return ok();
 }
 

@@ -16,6 +16,8 @@ struct State {
     int cu_count = 256;
     hipStream_t stream = nullptr;
     int *flag = nullptr;
+    // Device address of `scratch` on each device the library initialised.
+    std::unordered_map<int, float *> scratch_by_device;
     // Pool: exact-size free lists over rounded sizes; blocks never shrink.
     std::unordered_map<size_t, std::vector<void *>> free_lists;
     std::unordered_map<void *, size_t> live;
@@ -29,6 +31,17 @@ State &state() {
 }
 
 thread_local std::string t_last_error;
+
+} // namespace
+
+// Scratch of the allocation-free entry points (camel_hip_sgemm_noalloc):
+// their split-K partial sums live here instead of in pool blocks.  Every
+// device the library runs on holds its own copy of this array until the
+// process ends; host code never uses this name as an address, only the
+// per-device address hipGetSymbolAddress gives for it at initialisation.
+static __device__ __align__(256) float scratch[CAMEL_HIP_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
 
 // Rounded block size: 512 B granules below 1 MiB, 2 MiB granules above, so
 // tensors of one shape reuse one block and large tensors do not fragment.
@@ -96,6 +109,13 @@ int init_device(int device) {
     CAMEL_RETURN_IF(check_hip(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking),
                               "hipStreamCreateWithFlags"));
     CAMEL_RETURN_IF(check_hip(hipMalloc(&s.flag, 256), "hipMalloc(error flag)"));
+    // The static scratch's address on this device (the device is current).
+    void *scratch_ptr = nullptr;
+    CAMEL_RETURN_IF(check_hip(hipGetSymbolAddress(&scratch_ptr, HIP_SYMBOL(scratch)),
+                              "hipGetSymbolAddress(scratch)"));
+    if (!scratch_ptr || (reinterpret_cast<uintptr_t>(scratch_ptr) & 255) != 0)
+        return fail(CAMEL_HIP_ERR_RUNTIME, "camel_hip_init: static scratch is not 256-byte aligned");
+    s.scratch_by_device[device] = static_cast<float *>(scratch_ptr);
     s.device = device;
     s.initialised = true;
     return clear_error_flag();
@@ -107,6 +127,19 @@ int ensure_init() {
     CAMEL_LOCK();
     if (state().initialised) return CAMEL_HIP_OK;
     return init_device(0);
+}
+
+bool initialised() {
+    CAMEL_LOCK();
+    return state().initialised;
+}
+
+float *noalloc_scratch() {
+    CAMEL_LOCK();
+    const State &s = state();
+    if (!s.initialised) return nullptr;
+    auto it = s.scratch_by_device.find(s.device);
+    return it == s.scratch_by_device.end() ? nullptr : it->second;
 }
 
 int clear_error_flag() {

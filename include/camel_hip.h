@@ -124,6 +124,26 @@ int camel_hip_arange(int64_t *out, int64_t start, int64_t step, int64_t count);
  * (test/run/nn/svm.cml:31), both fused in the GEMM epilogue. */
 int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
                     const float *bias, int flags);
+/* Bytes of the static scratch of the allocation-free entry points (one copy
+ * per device the library runs on, held until the process ends). */
+#define CAMEL_HIP_NOALLOC_SCRATCH_BYTES (64u << 20)
+/* camel_hip_sgemm without any device allocation: the same kernels and the
+ * same results bit for bit, with split-K partial sums kept in the library's
+ * static scratch (CAMEL_HIP_NOALLOC_SCRATCH_BYTES) instead of pool blocks.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  camel_hip_init must have run first (initialisation allocates).
+ * A shape whose split-K partials need more than the scratch is refused with
+ * CAMEL_HIP_ERR_SHAPE before anything is launched (no benchmark shape comes
+ * near it: the most any GEMM schedule uses is 64 MiB, a full round of split
+ * 256x256 tiles).  Every call on a device shares that device's scratch, which
+ * keeps the last call's contents (nothing in it needs to start at zero).
+ * Library calls run in order on the library stream, but work that overlaps
+ * on one device -- e.g. a graph captured from this entry point replayed on
+ * another stream while the library stream runs another such call -- races
+ * on the scratch. */
+int camel_hip_sgemm_noalloc(const float *A, const float *B, float *C, int64_t M, int64_t N,
+                            int64_t K, const float *bias, int flags);
 /* C[M,N] = softmax_rows(A . B (+bias) (relu)): the dense..softmax of a
  * classifier layer (README.md:43, `dense<w3, b3>..softmax`; softmax as in
  * test/run/nn/mnist.cml:13-25) fused into one pass when N <= 32 (each row's

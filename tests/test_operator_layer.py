@@ -356,3 +356,19 @@ def test_failed_operator_releases_what_it_made():
     with pytest.raises(T.CamelError, match="concat requires equal non-axis dimensions"):
         T.call("concat", arr, x, 0)
     assert T.live_count() == before
+
+
+def test_noalloc_sgemm_refuses_before_initialisation():
+    # Initialisation allocates (stream, error flag), so the allocation-free
+    # entry point will not do it: a fresh process that never initialised the
+    # library gets an error and no device work.
+    import subprocess
+    import sys
+    code = ("import ctypes as C; from camel_amd import _hip as H; L = H.load(); p = C.c_void_p(256); "
+            "rc = L.camel_hip_sgemm_noalloc(p, p, p, 4, 4, 4, None, 0); "
+            "print(rc, L.camel_hip_last_error().decode())")
+    out = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    rc, msg = out.stdout.strip().split(" ", 1)
+    assert int(rc) == H.ERR_ARG and "camel_hip_init" in msg
