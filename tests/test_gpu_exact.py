@@ -333,3 +333,20 @@ def test_cnn_chain_full_batch_is_exact(_release):
     softmax_close(full(t(x)).numpy(), logits)
     head.release()
     full.release()
+
+
+@pytest.mark.parametrize("M,N,Kd", [(16, 4096, 4096), (32, 4096, 8192), (8, 1000, 20000)])
+def test_skinny_split_sums_are_exact_on_every_call(M, N, Kd):
+    # The streaming kernel's k partials and their ordered reduce: 40 calls in
+    # a row into an output pre-filled with NaN, each bit-exact (a partial read
+    # before its writer finished would show up here).
+    a, b = ints(M * Kd, (M, Kd)), ints(N + Kd, (Kd, N))
+    bias = ints(N, (N,))
+    want = exact_dense(a, b, bias, True)
+    da, db, dbias = K.dev(a), K.dev(b), K.dev(bias)
+    dc = K.empty(M * N * 4)
+    for i in range(40):
+        H.call("camel_hip_fill", H.DT_F32, P(dc.ptr), M * N, float("nan"))
+        H.call("camel_hip_sgemm", P(da.ptr), P(db.ptr), P(dc.ptr), M, N, Kd, P(dbias.ptr),
+               H.EPI_BIAS | H.EPI_RELU)
+        assert_bits(K.host(dc, F, (M, N)), want, f"call {i}")
