@@ -46,16 +46,25 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E, vendor figure
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.txt")
 
 
-def _traffic(key: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.txt)."""
+def _traffic_entry(key: str):
+    """(HBM bytes per call, provenance) from profiles/traffic.txt, measured with
+    two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE); provenance names the
+    commit the counters were read at and the kernels they cover."""
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
-                if line.startswith(key + ":"):
-                    return float(line.split(":", 1)[1].split()[0])
+                if not line.startswith(key + ":"):
+                    continue
+                fields = line.split(":", 1)[1].split()
+                src = {"file": "profiles/traffic.txt", "counters": "FETCH_SIZE, WRITE_SIZE"}
+                for fld in fields[4:]:
+                    if "=" in fld:
+                        k, v = fld.split("=", 1)
+                        src[k] = v.split(",") if k == "kernels" else v
+                return float(fields[0]), src
     except OSError:
         pass
-    return None
+    return None, None
 
 
 def _progress(msg: str) -> None:
@@ -100,16 +109,27 @@ def sgemm_call(da, db, dc, M, N, K, dbias=None, flags=0):
                           P(dbias.ptr) if dbias is not None else None, flags)
 
 
-def roofline_mfma(flop: float, ms: float, traffic=None):
+def _with_traffic(line: dict, key):
+    if key is not None:
+        nbytes, src = _traffic_entry(key)
+        line["traffic"] = nbytes
+        if src is not None:
+            line["traffic_source"] = src
+    return line
+
+
+def roofline_mfma(flop: float, ms: float, traffic_key=None):
     ach = flop / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_MFMA_F32_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_F32_TFLOPS, 4), "traffic": traffic}
+    return _with_traffic({"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_MFMA_F32_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_F32_TFLOPS, 4),
+                          "traffic": None}, traffic_key)
 
 
-def roofline_hbm(nbytes: float, ms: float, traffic=None):
+def roofline_hbm(nbytes: float, ms: float, traffic_key=None):
     ach = nbytes / (ms * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic}
+    return _with_traffic({"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
+                          "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None},
+                         traffic_key)
 
 
 # ---------------------------------------------------------------- workloads
@@ -312,26 +332,122 @@ def wl_softmax(steps, warmup):
 
 
 # ------------------------------------------------------------- CPU baseline
+#
+# The oracle (a loop-for-loop restatement of the reference's CPU kernels:
+# ijk matmul with fp64 accumulation and per-element dtype dispatch,
+# operators.cpp:757-766; tensorBinary, runtime.cpp:775-793; the mnist.cml
+# softmax composition; conv2d as direct loops in matmul order), single
+# thread, on this host, in this run -- a reported baseline per suite row,
+# full where it finishes in seconds, otherwise a labelled slab of the same
+# workload whose cost per row / image / element is the same as the whole's.
 
-def cpu_baseline_gemm(a, b, budget_s: float = 12.0):
-    """Oracle ijk matmul (reference operators.cpp:757-766) on a row slab, 1 thread."""
-    from oracle import ffi as O  # the CPU baseline leg is the only bench user of the oracle
+def _oracle():
+    from oracle import ffi as O  # the CPU baseline leg is bench.py's only user of the oracle
+    return O
+
+
+def _cpu_line(value: float, unit: str, sample: str, spent: float) -> dict:
+    n = os.cpu_count()
+    return {"value": round(value, 4), "unit": unit, "cores": 1, "nproc": n, "kind": "port",
+            "sample": f"{sample}; {spent:.2f} s on 1 of {n} host cores"}
+
+
+def _timed(fn):
+    t0 = time.perf_counter()
+    out = fn()
+    return out, time.perf_counter() - t0
+
+
+def cpu_baseline_gemm(a, b, budget_s: float = 12.0, max_rows: int | None = None):
+    """Oracle ijk matmul (reference operators.cpp:757-766) on a row slab, 1 thread:
+    as many leading rows as fit the budget (all of them for small problems)."""
+    O = _oracle()
     M, K = a.shape
     N = b.shape[1]
-    rows, spent = 0, 0.0
-    t0 = time.perf_counter()
-    O.matmul_rows(a, b, 0, 1)  # warm
-    per_row = time.perf_counter() - t0
-    target = max(1, min(M, int(budget_s / max(per_row, 1e-6))))
-    t0 = time.perf_counter()
-    O.matmul_rows(a, b, 0, target)
-    spent = time.perf_counter() - t0
-    rows = target
-    gflops = 2.0 * rows * N * K / spent / 1e9
-    return {"value": round(gflops, 4), "unit": "GFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"rows 0-{rows - 1} of the {M}x{N}x{K} fp32 matmul through the oracle "
-                      f"(ijk, fp64 accumulate, per-element dtype dispatch), {spent:.1f} s on 1 of "
-                      f"{os.cpu_count()} host cores"}
+    _, per_row = _timed(lambda: O.matmul_rows(a, b, 0, 1))
+    rows = max(1, min(M, int(budget_s / max(per_row, 1e-6)), max_rows or M))
+    _, spent = _timed(lambda: O.matmul_rows(a, b, 0, rows))
+    what = "all rows" if rows == M else f"rows 0-{rows - 1} (slab, extrapolated per row)"
+    return _cpu_line(2.0 * rows * N * K / spent / 1e9, "GFLOP/s",
+                     f"{what} of the {M}x{N}x{K} fp32 matmul through the oracle (ijk, fp64 "
+                     f"accumulate, per-element dtype dispatch)", spent)
+
+
+def cpu_baseline_mlp(x, ws, bs):
+    """The whole MLP forward (config 2) through the oracle: three dense layers
+    (matmul + bias, relu as x*(x>0)) and the mnist.cml softmax composition."""
+    O = _oracle()
+
+    def run():
+        h = x
+        for i in range(3):
+            h = O.dense(h, ws[i], bs[i], i < 2)
+        return O.softmax_rows(h)
+
+    _, spent = _timed(run)
+    flop = sum(2.0 * x.shape[0] * w.shape[0] * w.shape[1] for w in ws)
+    return _cpu_line(flop / spent / 1e9, "GFLOP/s",
+                     f"full MLP forward, batch {x.shape[0]} (784->1024->1024->10 + softmax)", spent)
+
+
+def cpu_baseline_conv(x, w, b, images: int = 1):
+    """conv2d config 4 through the oracle's direct loops on an image slab."""
+    O = _oracle()
+    _, spent = _timed(lambda: O.conv2d_images(x, w, b, True, 0, images, 1, 1))
+    N, Cin, H_, W_ = x.shape
+    Co = w.shape[0]
+    flop = 2.0 * images * H_ * W_ * Co * Cin * 9
+    return _cpu_line(flop / spent / 1e9, "GFLOP/s",
+                     f"images 0-{images - 1} of {N} (slab, extrapolated per image) of the "
+                     f"{N}x{Cin}x{H_}x{W_} -> {Co} 3x3 conv + bias + relu", spent)
+
+
+def cpu_baseline_cnn(images: int = 32):
+    """The CNN forward (config 5) through the oracle on an image slab: conv,
+    conv, 2x2 pool, dense, dense, softmax, per image as the batch would run."""
+    O = _oracle()
+    x = D.uniform(D.SEED_CNN, (images, 1, 28, 28), 0.0, 1.0)
+    w1 = D.normal(D.SEED_CNN + 1, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
+    w2 = D.normal(D.SEED_CNN + 2, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288)))
+    w3 = D.normal(D.SEED_CNN + 3, (9216, 128), std=float(np.sqrt(2.0 / 9216)))
+    w4 = D.normal(D.SEED_CNN + 4, (128, 10), std=float(np.sqrt(2.0 / 128)))
+    z = lambda n: np.zeros(n, np.float32)
+
+    def run():
+        h = O.conv2d(x, w1, z(32), True)
+        h = O.conv2d(h, w2, z(64), True)
+        h = O.maxpool2d(h, 2, 2).reshape(images, 9216)
+        h = O.dense(h, w3, z(128), True)
+        return O.softmax_rows(O.dense(h, w4, z(10), False))
+
+    _, spent = _timed(run)
+    flop = 2.0 * images * (26 * 26 * 32 * 9 + 24 * 24 * 64 * 288 + 9216 * 128 + 128 * 10)
+    return _cpu_line(flop / spent / 1e9, "GFLOP/s",
+                     f"images 0-{images - 1} of 512 (slab, extrapolated per image) of the CNN "
+                     f"forward", spent)
+
+
+def cpu_baseline_bandwidth(kind: str, n: int = 1 << 24):
+    """Elementwise / softmax through the oracle on the first n elements of the
+    same seeded inputs, in the suite line's unit (GB/s of algorithmic bytes)."""
+    O = _oracle()
+    if kind == "softmax":
+        x = D.normal(D.SEED_ELT + 2, (n // 1024, 1024))
+        _, spent = _timed(lambda: O.softmax_rows(x))
+        return _cpu_line(8.0 * n / spent / 1e9, "GB/s",
+                         f"rows 0-{n // 1024 - 1} of 262144 (slab) of the 1024-column row softmax "
+                         f"(mnist.cml composition)", spent)
+    a = D.uniform(D.SEED_ELT, (n,), -1.0, 1.0)
+    if kind == "relu":
+        _, spent = _timed(lambda: O.relu(a))
+        nbytes = 8.0 * n
+    else:
+        b = D.uniform(D.SEED_ELT + 1, (n,), -1.0, 1.0)
+        op = O.ADD if kind == "add" else O.MUL
+        _, spent = _timed(lambda: O.binary(op, a, b))
+        nbytes = 12.0 * n
+    return _cpu_line(nbytes / spent / 1e9, "GB/s",
+                     f"first {n} of 2^28 elements (slab) of {kind}", spent)
 
 
 # ------------------------------------------------------------------- main
@@ -385,23 +501,28 @@ def main() -> int:
         "data": "synthetic (seeded SplitMix64 U(-1,1), generated on host, resident in HBM)",
         "config": {"workload": "sgemm M=N=K=4096 (BASELINE config 3)", "M": 4096, "N": 4096,
                    "K": 4096, "layout": "row-major contiguous", "parallelism": "single GPU"},
-        "roofline": roofline_mfma(g["flop"], g["ms"], _traffic("sgemm_4096")),
+        "roofline": roofline_mfma(g["flop"], g["ms"], "sgemm_4096"),
     }
     if not args.no_suite:
         global _suite_mode
         _suite_mode = True
         suite = {}
+        # CPU baselines of the suite rows run after all GPU work (see below).
+        cpu_jobs = []
         s_steps, s_warm = max(5, steps // 5), 2
         for n in (1024, 2048, 8192):
             r = wl_gemm(n, n, n, s_steps if n < 8192 else 5, s_warm)
             suite[f"sgemm_{n}"] = {"value": round(r["value"], 1), "unit": "GFLOP/s",
                                    "ms": round(r["ms"], 4),
                                    "roofline": roofline_mfma(r["flop"], r["ms"])}
+            cpu_jobs.append((f"sgemm_{n}", lambda a=r["a"], b=r["b"], n=n: cpu_baseline_gemm(
+                a, b, budget_s=4.0 if n == 1024 else 2.0)))
         r = wl_gemm(256, 256, 256, s_steps, s_warm)
         suite["matmul_256"] = {"value": round(r["value"], 1), "unit": "GFLOP/s",
                                "ms": round(r["ms"], 4),
                                "note": "BASELINE config 1 (plumbing anchor): launch-latency bound",
                                "roofline": roofline_mfma(r["flop"], r["ms"])}
+        cpu_jobs.append(("matmul_256", lambda a=r["a"], b=r["b"]: cpu_baseline_gemm(a, b)))
         r = wl_gemm_host(4096, 5, 2)
         suite["sgemm_4096_host_operands"] = {
             "value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1), "unit": "GFLOP/s",
@@ -412,11 +533,16 @@ def main() -> int:
         suite["sgemm_16x4096x4096"] = {
             "value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1), "unit": "GFLOP/s",
             "ms": round(r["ms"], 4),
-            "roofline": roofline_hbm(r["bytes"], r["ms"], _traffic("skinny"))}
+            "roofline": roofline_hbm(r["bytes"], r["ms"], "skinny")}
+        cpu_jobs.append(("sgemm_16x4096x4096", lambda: cpu_baseline_gemm(
+            D.uniform(D.SEED_GEMM + 16, (16, 4096), -1.0, 1.0),
+            D.uniform(D.SEED_GEMM + 17, (4096, 4096), -1.0, 1.0))))
         r = wl_mlp(s_steps * 2, s_warm)
         suite["mlp_forward"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                 "unit": "GFLOP/s", "ms": round(r["ms"], 4),
-                                "roofline": roofline_mfma(r["flop"], r["ms"], _traffic("mlp"))}
+                                "roofline": roofline_mfma(r["flop"], r["ms"], "mlp")}
+        cpu_jobs.append(("mlp_forward", lambda x=r["x"], ws=r["ws"], bs=r["bs"]:
+                         cpu_baseline_mlp(x, ws, bs)))
         r = wl_mlp(s_steps * 2, s_warm, fused=False)
         suite["mlp_forward_unfused"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                         "unit": "GFLOP/s", "ms": round(r["ms"], 4),
@@ -425,11 +551,14 @@ def main() -> int:
         r = wl_conv(s_steps, s_warm)
         suite["conv2d_3x3"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                "unit": "GFLOP/s", "ms": round(r["ms"], 4),
-                               "roofline": roofline_mfma(r["flop"], r["ms"], _traffic("conv2d"))}
+                               "roofline": roofline_mfma(r["flop"], r["ms"], "conv2d")}
+        cpu_jobs.append(("conv2d_3x3", lambda x=r["x"], w=r["w"], b=r["b"]:
+                         cpu_baseline_conv(x, w, b, images=2)))
         r = wl_cnn(s_steps, s_warm)
         suite["cnn_forward"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                 "unit": "GFLOP/s", "ms": round(r["ms"], 4),
-                                "roofline": roofline_mfma(r["flop"], r["ms"], _traffic("cnn"))}
+                                "roofline": roofline_mfma(r["flop"], r["ms"], "cnn")}
+        cpu_jobs.append(("cnn_forward", lambda: cpu_baseline_cnn(images=32)))
         r = wl_cnn(s_steps, s_warm, fused=False)
         suite["cnn_forward_unfused"] = {"value": round(r["flop"] / (r["ms"] * 1e-3) / 1e9, 1),
                                         "unit": "GFLOP/s", "ms": round(r["ms"], 4),
@@ -440,12 +569,14 @@ def main() -> int:
             suite[f"eltwise_{name}"] = {"value": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1),
                                         "unit": "GB/s", "ms": round(r["ms"], 4),
                                         "roofline": roofline_hbm(r["bytes"], r["ms"],
-                                                                 _traffic(f"eltwise_{name}"))}
+                                                                 f"eltwise_{name}")}
+            cpu_jobs.append((f"eltwise_{name}", lambda name=name: cpu_baseline_bandwidth(name)))
         r = wl_softmax(s_steps, s_warm)
         suite["softmax_262144x1024"] = {"value": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1),
                                         "unit": "GB/s", "ms": round(r["ms"], 4),
                                         "roofline": roofline_hbm(r["bytes"], r["ms"],
-                                                                 _traffic("softmax"))}
+                                                                 "softmax")}
+        cpu_jobs.append(("softmax_262144x1024", lambda: cpu_baseline_bandwidth("softmax")))
         line["suite"] = suite
         for k, v in suite.items():
             _progress(f"{k}: {v['value']} {v['unit']} ({100 * v['roofline']['frac']:.1f}% of peak)")
@@ -455,6 +586,11 @@ def main() -> int:
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_gemm(g["a"], g["b"])
         _progress(f"cpu baseline: {line['cpu_baseline']['value']} GFLOP/s")
+        if not args.no_suite:
+            for key, job in cpu_jobs:
+                line["suite"][key]["cpu_baseline"] = job()
+                _progress(f"cpu baseline {key}: {line['suite'][key]['cpu_baseline']['value']} "
+                          f"{line['suite'][key]['cpu_baseline']['unit']}")
     del g
 
     print(json.dumps(line), flush=True)
