@@ -23,6 +23,7 @@ DT_F32, DT_I64, DT_BOOL = 0, 1, 2
 OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_POW = range(5)
 CMP_LT, CMP_LE, CMP_GT, CMP_GE, CMP_EQ = range(5)
 EPI_NONE, EPI_BIAS, EPI_RELU = 0, 1, 2
+GEMM_A_T = 0x10
 CONV_X_NHWC, CONV_Y_NHWC, CONV_W_PACKED = 0x100, 0x200, 0x400
 CONV_X_NCHW4, CONV_Y_NCHW4 = 0x800, 0x1000
 

@@ -53,10 +53,15 @@ constexpr int GROUP_M = 4;
 // LOAD_PLANES_POOL read NCHW x in place with the same K order: a k-quad of a
 // pixel is 4 loads from 4 channel planes, and a wave's lanes take consecutive
 // pixels, so each load instruction reads a contiguous run of one plane.
+// LOAD_TVEC / LOAD_TSCALAR (A operand only) read A given transposed, as
+// At [K, M] row-major (A[m][k] = At[k][m]): like B, k rows with the tile's
+// m contiguous, transposed 4x4 in registers before the LDS store, so
+// transpose(X) @ E needs no copy of X (16-byte loads need M % 4 == 0).
 enum {
     LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3, LOAD_NHWC_POOL = 4,
-    LOAD_PLANES = 5, LOAD_PLANES_POOL = 6
+    LOAD_PLANES = 5, LOAD_PLANES_POOL = 6, LOAD_TVEC = 7, LOAD_TSCALAR = 8
 };
+template <int M> constexpr bool is_trans = (M == LOAD_TVEC || M == LOAD_TSCALAR);
 
 // Loaders that take (pixel, k-quad) items over K ordered (kh, kw, c).
 template <int M>
@@ -87,18 +92,22 @@ struct Tile {
     static constexpr int A_TOTAL = BM * KQ;
     static constexpr int B_TOTAL = KQ * (BN / 4);
     static constexpr int BN_TOTAL = BN * KQ; // B as pixel rows (LOAD_NHWC)
+    static constexpr int A_T_TOTAL = KQ * (BM / 4); // A given transposed: 4 k rows x 4 m
     static constexpr int A_ITEMS = (A_TOTAL + THREADS - 1) / THREADS;
+    static constexpr int A_T_ITEMS = (A_T_TOTAL + THREADS - 1) / THREADS;
     static constexpr int B_ITEMS = (B_TOTAL + THREADS - 1) / THREADS;
     static constexpr int BN_ITEMS = (BN_TOTAL + THREADS - 1) / THREADS;
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
     static_assert(BN % 32 == 0, "B column swizzle works on aligned runs of 32 columns");
     static_assert(BK % (8 * WK) == 0, "each wave k-group takes whole 8-k groups of a stage");
     static_assert(A_TOTAL % 64 == 0 && B_TOTAL % 64 == 0, "item guards must be wave-uniform");
+    static_assert(A_T_TOTAL % 64 == 0, "transposed-A item guards must be wave-uniform");
     static_assert((WK - 1) * BM * BN <= 2 * STAGE, "k-group reduction must fit the LDS buffers");
 };
 
 struct GemmArgs {
-    const float *A;  // [M, lda] row-major (conv: weights [Co, C*KH*KW])
+    const float *A;  // [M, lda] row-major (conv: weights [Co, C*KH*KW]); transposed
+                     // loaders: At [K, lda] row-major with lda >= M
     const float *B;  // [K, ldb] row-major (conv: input x, NCHW)
     float *C;        // [M, ldc] row-major (conv: output y, NCHW)
     const float *bias;
@@ -222,10 +231,16 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     // Items past a stage's count (when THREADS does not divide it) are skipped
     // by whole waves.
     constexpr bool A_TAIL = T::A_TOTAL % T::THREADS != 0;
+    constexpr bool AT_TAIL = T::A_T_TOTAL % T::THREADS != 0;
     constexpr bool B_TAIL = T::B_TOTAL % T::THREADS != 0;
+    if constexpr (is_trans<AMODE>) {
+        static_assert(T::THREADS % (T::BM / 4) == 0 || (T::BM / 4) % T::THREADS == 0,
+                      "transposed A column mapping");
+    }
     // One stage of operands in flight from global memory to LDS.
     struct StageRegs {
-        float4 ra[T::A_ITEMS];
+        float4 ra[is_trans<AMODE> ? 1 : T::A_ITEMS];
+        float4 rat[is_trans<AMODE> ? T::A_T_ITEMS : 1][4];
         float4 rb[is_nhwc<BMODE> ? 1 : T::B_ITEMS][4];
         float4 rbn[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
     };
@@ -300,10 +315,38 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     auto load_stage = [&](auto full_tag, int k0, StageRegs &R) {
         constexpr bool FULL = decltype(full_tag)::value;
         float4 *ra = R.ra;
+        auto &rat = R.rat;
         auto &rb = R.rb;
         float4 *rbn = R.rbn;
 #pragma unroll
-        for (int i = 0; i < T::A_ITEMS; ++i) {
+        for (int i = 0; i < (is_trans<AMODE> ? T::A_T_ITEMS : 0); ++i) {
+            // item (kq, mq): rows k0+4kq .. +3 of At, columns m0+4mq .. +3
+            // (vector) or m0+mq+c*BM/4 (scalar, c = 0..3)
+            const int q = tid + i * T::THREADS;
+            if (AT_TAIL && q >= T::A_T_TOTAL) break;
+            const int mq = q % (T::BM / 4), kq = q / (T::BM / 4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int gk = k0 + 4 * kq + u;
+                const float *row = g.A + (size_t)gk * g.lda;
+                if constexpr (AMODE == LOAD_TVEC) {
+                    const int gm = m0 + 4 * mq;
+                    rat[i][u] = (FULL || (gm < g.M && gk >= 0 && gk < kend))
+                                    ? *reinterpret_cast<const float4 *>(row + gm)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    float v[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int gm = m0 + mq + c * (T::BM / 4);
+                        v[c] = (FULL || (gm < g.M && gk >= 0 && gk < kend)) ? row[gm] : 0.f;
+                    }
+                    rat[i][u] = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (is_trans<AMODE> ? 0 : T::A_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             if (A_TAIL && q >= T::A_TOTAL) break;
             const int kq = q % T::KQ, m = q / T::KQ;
@@ -392,10 +435,30 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 
     auto store_stage = [&](float *As, float *Bs, const StageRegs &R) {
         const float4 *ra = R.ra;
+        const auto &rat = R.rat;
         const auto &rb = R.rb;
         const float4 *rbn = R.rbn;
 #pragma unroll
-        for (int i = 0; i < T::A_ITEMS; ++i) {
+        for (int i = 0; i < (is_trans<AMODE> ? T::A_T_ITEMS : 0); ++i) {
+            const int q = tid + i * T::THREADS;
+            if (AT_TAIL && q >= T::A_T_TOTAL) break;
+            const int mq = q % (T::BM / 4), kq = q / (T::BM / 4);
+            float *plane = As + kq * T::A_PLANE;
+            // rat[i][u] holds k row k0+4kq+u for 4 m; LDS wants, per m, the 4
+            // k values as one chunk: a 4x4 transpose in registers.
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int m = (AMODE == LOAD_TVEC) ? 4 * mq + c : mq + c * (T::BM / 4);
+                float4 col;
+                col.x = rat[i][0][c];
+                col.y = rat[i][1][c];
+                col.z = rat[i][2][c];
+                col.w = rat[i][3][c];
+                *reinterpret_cast<float4 *>(plane + m * 4) = col;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < (is_trans<AMODE> ? 0 : T::A_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             if (A_TAIL && q >= T::A_TOTAL) break;
             const int kq = q % T::KQ, m = q / T::KQ;
@@ -1925,7 +1988,16 @@ template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, co
     return CAMEL_HIP_OK;
 }
 
-template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool bvec) {
+// Runs the tile GEMM with the loaders the operands allow: A row-major or
+// (atrans) given transposed, each with 16-byte loads where avec / bvec.
+template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool bvec,
+                                         bool atrans = false) {
+    if (atrans) {
+        if (avec && bvec) return run_gemm<T, LOAD_TVEC, LOAD_VEC>(g, splits, "sgemm_kernel");
+        if (avec) return run_gemm<T, LOAD_TVEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
+        if (bvec) return run_gemm<T, LOAD_TSCALAR, LOAD_VEC>(g, splits, "sgemm_kernel");
+        return run_gemm<T, LOAD_TSCALAR, LOAD_SCALAR>(g, splits, "sgemm_kernel");
+    }
     if (avec && bvec) return run_gemm<T, LOAD_VEC, LOAD_VEC>(g, splits, "sgemm_kernel");
     if (avec) return run_gemm<T, LOAD_VEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
     if (bvec) return run_gemm<T, LOAD_SCALAR, LOAD_VEC>(g, splits, "sgemm_kernel");
@@ -1933,9 +2005,19 @@ template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool
 }
 
 // Partial-sum bytes launch_gemm_modes<T> will need for these arguments.
-template <class T> size_t gemm_modes_partial_bytes(const GemmArgs &g, int splits, bool avec, bool bvec) {
+template <class T> size_t gemm_modes_partial_bytes(const GemmArgs &g, int splits, bool avec,
+                                                   bool bvec, bool atrans = false) {
     GemmSchedule s;
-    if (avec && bvec)
+    if (atrans) {
+        if (avec && bvec)
+            s = schedule_gemm<T, LOAD_TVEC, LOAD_VEC>(g, splits);
+        else if (avec)
+            s = schedule_gemm<T, LOAD_TVEC, LOAD_SCALAR>(g, splits);
+        else if (bvec)
+            s = schedule_gemm<T, LOAD_TSCALAR, LOAD_VEC>(g, splits);
+        else
+            s = schedule_gemm<T, LOAD_TSCALAR, LOAD_SCALAR>(g, splits);
+    } else if (avec && bvec)
         s = schedule_gemm<T, LOAD_VEC, LOAD_VEC>(g, splits);
     else if (avec)
         s = schedule_gemm<T, LOAD_VEC, LOAD_SCALAR>(g, splits);
@@ -2395,6 +2477,8 @@ int conv2d_run(const float *x, const float *w, const float *bias, float *y, int6
 int sgemm_check(const float *A, const float *B, const float *C, int64_t M, int64_t N, int64_t K,
                 const float *bias, int flags, const char *name) {
     const std::string who(name);
+    if (flags & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU | CAMEL_GEMM_A_T))
+        return fail(CAMEL_HIP_ERR_ARG, who + ": unknown flags");
     if (M < 0 || N < 0 || K < 0) return fail(CAMEL_HIP_ERR_SHAPE, who + ": negative dimension");
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
         return fail(CAMEL_HIP_ERR_SHAPE, who + ": dimension too large");
@@ -2414,10 +2498,10 @@ GemmArgs sgemm_args(const float *A, const float *B, float *C, int64_t M, int64_t
     g.M = (int)M;
     g.N = (int)N;
     g.K = (int)K;
-    g.lda = (int)K;
+    g.lda = (flags & CAMEL_GEMM_A_T) ? (int)M : (int)K;
     g.ldb = (int)N;
     g.ldc = (int)N;
-    g.flags = flags;
+    g.flags = flags & (CAMEL_EPI_BIAS | CAMEL_EPI_RELU);
     return g;
 }
 
@@ -2428,40 +2512,42 @@ struct SgemmPlan {
     SgemmPath path;
     Cfg cfg;
     int splits;
-    bool avec, bvec;
+    bool avec, bvec, atrans;
     size_t partial_bytes;
 };
 
-SgemmPlan plan_sgemm(const GemmArgs &g) {
-    SgemmPlan p{SgemmPath::Tiles, Cfg::Big, 1, false, false, 0};
-    if (thin_eligible(g.M, g.N, g.K)) {
+// atrans: A is given transposed (CAMEL_GEMM_A_T); only the tile kernel has
+// the transposed loaders, so the thin and skinny kernels are not used.
+SgemmPlan plan_sgemm(const GemmArgs &g, bool atrans) {
+    SgemmPlan p{SgemmPath::Tiles, Cfg::Big, 1, false, false, atrans, 0};
+    if (!atrans && thin_eligible(g.M, g.N, g.K)) {
         p.path = SgemmPath::Thin;
         return p;
     }
-    if (skinny_eligible(g.M, g.N, g.K, g.B, g.C)) {
+    if (!atrans && skinny_eligible(g.M, g.N, g.K, g.B, g.C)) {
         p.path = SgemmPath::Skinny;
         p.partial_bytes = skinny_partial_bytes(g.M, g.N, g.K);
         return p;
     }
-    p.avec = (g.K % 4 == 0) && ((uintptr_t)g.A % 16 == 0);
+    p.avec = ((atrans ? g.M : g.K) % 4 == 0) && ((uintptr_t)g.A % 16 == 0);
     p.bvec = (g.N % 4 == 0) && ((uintptr_t)g.B % 16 == 0);
     int bk = 0;
     choose(g.M, g.N, g.K, device_cu_count(), p.cfg, p.splits, bk);
     switch (p.cfg) {
     case Cfg::Big:
-        p.partial_bytes = gemm_modes_partial_bytes<TileBig>(g, p.splits, p.avec, p.bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileBig>(g, p.splits, p.avec, p.bvec, atrans);
         break;
     case Cfg::Mid:
-        p.partial_bytes = gemm_modes_partial_bytes<TileMid>(g, p.splits, p.avec, p.bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileMid>(g, p.splits, p.avec, p.bvec, atrans);
         break;
     case Cfg::Tiny:
-        p.partial_bytes = gemm_modes_partial_bytes<TileTiny>(g, p.splits, p.avec, p.bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileTiny>(g, p.splits, p.avec, p.bvec, atrans);
         break;
     case Cfg::Small:
-        p.partial_bytes = gemm_modes_partial_bytes<TileSmall>(g, p.splits, p.avec, p.bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileSmall>(g, p.splits, p.avec, p.bvec, atrans);
         break;
     default:
-        p.partial_bytes = gemm_modes_partial_bytes<TileSkinny>(g, p.splits, p.avec, p.bvec);
+        p.partial_bytes = gemm_modes_partial_bytes<TileSkinny>(g, p.splits, p.avec, p.bvec, atrans);
         break;
     }
     return p;
@@ -2478,15 +2564,15 @@ int run_sgemm(const GemmArgs &g, const SgemmPlan &p) {
     }
     switch (p.cfg) {
     case Cfg::Big:
-        return launch_gemm_modes<TileBig>(g, p.splits, p.avec, p.bvec);
+        return launch_gemm_modes<TileBig>(g, p.splits, p.avec, p.bvec, p.atrans);
     case Cfg::Mid:
-        return launch_gemm_modes<TileMid>(g, p.splits, p.avec, p.bvec);
+        return launch_gemm_modes<TileMid>(g, p.splits, p.avec, p.bvec, p.atrans);
     case Cfg::Tiny:
-        return launch_gemm_modes<TileTiny>(g, p.splits, p.avec, p.bvec);
+        return launch_gemm_modes<TileTiny>(g, p.splits, p.avec, p.bvec, p.atrans);
     case Cfg::Small:
-        return launch_gemm_modes<TileSmall>(g, p.splits, p.avec, p.bvec);
+        return launch_gemm_modes<TileSmall>(g, p.splits, p.avec, p.bvec, p.atrans);
     default:
-        return launch_gemm_modes<TileSkinny>(g, p.splits, p.avec, p.bvec);
+        return launch_gemm_modes<TileSkinny>(g, p.splits, p.avec, p.bvec, p.atrans);
     }
 }
 
@@ -2504,7 +2590,7 @@ int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
     const GemmArgs g = sgemm_args(A, B, C, M, N, K, bias, flags);
-    CAMEL_RETURN_IF(run_sgemm(g, plan_sgemm(g)));
+    CAMEL_RETURN_IF(run_sgemm(g, plan_sgemm(g, (flags & CAMEL_GEMM_A_T) != 0)));
     return ok();
 }
 
@@ -2519,7 +2605,7 @@ int camel_hip_sgemm_noalloc(const float *A, const float *B, float *C, int64_t M,
     float *scratch = noalloc_scratch();
     if (!scratch) return fail(CAMEL_HIP_ERR_RUNTIME, "sgemm_noalloc: static scratch not set up");
     const GemmArgs g = sgemm_args(A, B, C, M, N, K, bias, flags);
-    const SgemmPlan plan = plan_sgemm(g);
+    const SgemmPlan plan = plan_sgemm(g, (flags & CAMEL_GEMM_A_T) != 0);
     if (plan.partial_bytes > CAMEL_HIP_NOALLOC_SCRATCH_BYTES)
         return fail(CAMEL_HIP_ERR_SHAPE,
                     "sgemm_noalloc: this shape needs " + std::to_string(plan.partial_bytes) +

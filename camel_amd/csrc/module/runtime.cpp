@@ -130,10 +130,15 @@ TensorObject *tensorReshape(const TensorObject *tensor, std::span<const int64_t>
     return TensorObject::view(tensor, shape);
 }
 
-// tensorTranspose2D (runtime.cpp:704-720).
+// tensorTranspose2D (runtime.cpp:704-720).  Float32: a view, read in place
+// by matmul / dense (the GEMM's transposed-A loaders) and made contiguous by
+// any other reader; the reference's element copy through double is exact
+// for Float32.  Int64 and Bool are copied through double (int64 values past
+// 2^53 round, bools normalise to 0/1) as the reference does.
 TensorObject *tensorTranspose2D(const TensorObject *tensor) {
     if (tensor->rank() != 2)
         throw std::invalid_argument("transpose currently only supports rank-2 tensors");
+    if (tensor->dtype() == TypeCode::Float32) return TensorObject::transposedView(tensor);
     int64_t shape[] = {tensor->dim(1), tensor->dim(0)};
     TensorObject *out = deviceTensor(tensor->dtype(), shape);
     if (tensor->numel() > 0)
@@ -260,10 +265,14 @@ TensorObject *tensorMatmul(const TensorObject *lhs, const TensorObject *rhs) {
         return out;
     }
     if (lhs->dtype() == TypeCode::Float32 && rhs->dtype() == TypeCode::Float32) {
-        checkHip(camel_hip_sgemm(static_cast<const float *>(lhs->deviceData()),
+        // A transposed lhs (transpose(X) @ E) is read in place.
+        std::shared_ptr<Storage> keep;
+        bool lhsT = false;
+        const void *a = lhs->storedDeviceData(keep, lhsT);
+        checkHip(camel_hip_sgemm(static_cast<const float *>(a),
                                  static_cast<const float *>(rhs->deviceData()),
                                  static_cast<float *>(out->deviceOutput()), M, N, K, nullptr,
-                                 CAMEL_EPI_NONE));
+                                 lhsT ? CAMEL_GEMM_A_T : CAMEL_EPI_NONE));
     } else {
         checkHip(camel_hip_matmul_generic(hipDType(lhs->dtype()), lhs->deviceData(),
                                           hipDType(rhs->dtype()), rhs->deviceData(),
@@ -443,8 +452,12 @@ TensorObject *tensorDense(const TensorObject *x, const TensorObject *w, const Te
     int64_t shape[] = {M, N};
     TensorObject *out = deviceTensor(TypeCode::Float32, shape);
     if (M == 0 || N == 0) return out;
-    const int flags = (bias ? CAMEL_EPI_BIAS : 0) | (relu ? CAMEL_EPI_RELU : 0);
-    checkHip(camel_hip_sgemm(static_cast<const float *>(x->deviceData()),
+    std::shared_ptr<Storage> keep;
+    bool xT = false;
+    const void *a = x->storedDeviceData(keep, xT);
+    const int flags = (bias ? CAMEL_EPI_BIAS : 0) | (relu ? CAMEL_EPI_RELU : 0) |
+                      (xT ? CAMEL_GEMM_A_T : 0);
+    checkHip(camel_hip_sgemm(static_cast<const float *>(a),
                              static_cast<const float *>(w->deviceData()),
                              static_cast<float *>(out->deviceOutput()), M, N, K,
                              bias ? static_cast<const float *>(bias->deviceData()) : nullptr, flags));

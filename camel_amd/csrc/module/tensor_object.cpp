@@ -77,9 +77,79 @@ TensorObject *TensorObject::view(const TensorObject *src, std::span<const int64_
     const uint64_t numel = product(shape);
     if (numel != src->numel_) throw std::invalid_argument("reshape changes tensor element count");
     auto *t = new TensorObject(src->dtype_, std::vector<int64_t>(shape.begin(), shape.end()), numel,
-                               src->byteSize_, src->storage_);
+                               src->byteSize_, src->storage());
     registerObject(t);
     return t;
+}
+
+TensorObject *TensorObject::transposedView(const TensorObject *src) {
+    if (src->rank() != 2 || src->dtype_ != TypeCode::Float32)
+        throw std::invalid_argument("transposed view needs a rank-2 Float32 tensor");
+    std::shared_ptr<Storage> block;
+    bool srcTransposed = false;
+    {
+        std::lock_guard<std::mutex> lock(src->layoutMutex_);
+        block = src->storage_;
+        srcTransposed = src->transposed_.load(std::memory_order_relaxed);
+    }
+    // The transpose of a transposed view is its source's layout again.
+    auto *t = new TensorObject(src->dtype_, {src->shape_[1], src->shape_[0]}, src->numel_,
+                               src->byteSize_, std::move(block));
+    t->transposed_.store(!srcTransposed, std::memory_order_release);
+    registerObject(t);
+    return t;
+}
+
+void TensorObject::makeContiguous() const {
+    if (!transposed_.load(std::memory_order_acquire)) return;
+    std::lock_guard<std::mutex> lock(layoutMutex_);
+    if (!transposed_.load(std::memory_order_relaxed)) return;
+    // Stored as [dim1, dim0] row-major; the contiguous payload is its
+    // transpose, [dim0, dim1].
+    const int64_t storedRows = shape_[1], storedCols = shape_[0];
+    auto fresh = std::make_shared<Storage>(byteSize_);
+    {
+        Storage &src = *storage_;
+        std::lock_guard<std::mutex> slock(src.mutex);
+        if (src.devValid || !src.hostValid) {
+            ensureDevBlock(src);
+            ensureDevBlock(*fresh);
+            if (byteSize_ > 0)
+                checkHip(camel_hip_transpose2d(hipDType(dtype_), src.dev, fresh->dev, storedRows,
+                                               storedCols));
+            fresh->devValid = true;
+        } else {
+            ensureHostBlock(*fresh);
+            const auto *in = reinterpret_cast<const float *>(src.host.get());
+            auto *out = reinterpret_cast<float *>(fresh->host.get());
+            for (int64_t r = 0; r < storedRows; ++r)
+                for (int64_t c = 0; c < storedCols; ++c) out[c * storedRows + r] = in[r * storedCols + c];
+            fresh->hostValid = true;
+        }
+    }
+    storage_ = std::move(fresh);
+    transposed_.store(false, std::memory_order_release);
+}
+
+const std::shared_ptr<Storage> &TensorObject::storage() const {
+    makeContiguous();
+    return storage_;
+}
+
+const void *TensorObject::storedDeviceData(std::shared_ptr<Storage> &keep, bool &transposed) const {
+    {
+        std::lock_guard<std::mutex> lock(layoutMutex_);
+        keep = storage_;
+        transposed = transposed_.load(std::memory_order_relaxed);
+    }
+    Storage &s = *keep;
+    std::lock_guard<std::mutex> lock(s.mutex);
+    if (!s.devValid) {
+        ensureDevBlock(s);
+        if (s.bytes > 0) checkHip(camel_hip_h2d(s.dev, s.host.get(), s.bytes));
+        s.devValid = true;
+    }
+    return s.dev;
 }
 
 int64_t TensorObject::dim(size_t index) const {
@@ -92,6 +162,7 @@ bool TensorObject::sameShape(const TensorObject *other) const {
 }
 
 const void *TensorObject::deviceData() const {
+    makeContiguous();
     Storage &s = *storage_;
     std::lock_guard<std::mutex> lock(s.mutex);
     if (!s.devValid) {
@@ -103,6 +174,7 @@ const void *TensorObject::deviceData() const {
 }
 
 void *TensorObject::deviceOutput() {
+    makeContiguous();
     Storage &s = *storage_;
     std::lock_guard<std::mutex> lock(s.mutex);
     ensureDevBlock(s);
@@ -112,6 +184,7 @@ void *TensorObject::deviceOutput() {
 }
 
 const void *TensorObject::hostData() const {
+    makeContiguous();
     Storage &s = *storage_;
     std::lock_guard<std::mutex> lock(s.mutex);
     if (!s.hostValid) {
@@ -123,6 +196,7 @@ const void *TensorObject::hostData() const {
 }
 
 void *TensorObject::hostOutput() {
+    makeContiguous();
     Storage &s = *storage_;
     std::lock_guard<std::mutex> lock(s.mutex);
     ensureHostBlock(s);
@@ -131,19 +205,32 @@ void *TensorObject::hostOutput() {
     return s.host.get();
 }
 
+// Residency of the payload as stored (a transposed view is not made
+// contiguous by asking).
 bool TensorObject::hostValid() const {
-    std::lock_guard<std::mutex> lock(storage_->mutex);
-    return storage_->hostValid;
+    std::shared_ptr<Storage> block;
+    {
+        std::lock_guard<std::mutex> lock(layoutMutex_);
+        block = storage_;
+    }
+    std::lock_guard<std::mutex> lock(block->mutex);
+    return block->hostValid;
 }
 
 bool TensorObject::deviceValid() const {
-    std::lock_guard<std::mutex> lock(storage_->mutex);
-    return storage_->devValid;
+    std::shared_ptr<Storage> block;
+    {
+        std::lock_guard<std::mutex> lock(layoutMutex_);
+        block = storage_;
+    }
+    std::lock_guard<std::mutex> lock(block->mutex);
+    return block->devValid;
 }
 
 void TensorObject::readElement(uint64_t flatIndex, void *dst) const {
     if (flatIndex >= numel_) throw std::invalid_argument("Tensor flat index out of range");
     const size_t es = elementSize(dtype_);
+    makeContiguous();
     Storage &s = *storage_;
     std::lock_guard<std::mutex> lock(s.mutex);
     if (s.hostValid) {
@@ -224,7 +311,7 @@ bool TensorObject::equals(const TensorObject *other) const {
     if (this == other) return true;
     if (!other) return false;
     if (dtype_ != other->dtype_ || shape_ != other->shape_ || numel_ != other->numel_) return false;
-    if (byteSize_ == 0 || storage_ == other->storage_) return true;
+    if (byteSize_ == 0 || storage() == other->storage()) return true;
     return std::memcmp(hostData(), other->hostData(), byteSize_) == 0;
 }
 

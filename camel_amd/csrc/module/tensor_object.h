@@ -19,6 +19,7 @@
 #include "camel_core.h"
 #include "camel_dlpack.h"
 
+#include <atomic>
 #include <cstddef>
 #include <iosfwd>
 #include <memory>
@@ -68,6 +69,14 @@ class TensorObject {
                                 bool zeroInit = false);
     // A tensor of `shape` sharing `src`'s payload (numel must match).
     static TensorObject *view(const TensorObject *src, std::span<const int64_t> shape);
+    // The transpose of a rank-2 Float32 tensor as a view: shape [c, r] over
+    // src's [r, c] payload, no copy.  Kernels that read the stored layout
+    // (the GEMM's transposed-A loaders) take it as is (storedDeviceData); any
+    // other access first makes this tensor's payload contiguous, once, with a
+    // device transpose into a block of its own, so every other reader sees
+    // the reference's row-major contents (tensorTranspose2D copies,
+    // runtime.cpp:704-720; for Float32 the copy through double is exact).
+    static TensorObject *transposedView(const TensorObject *src);
 
     size_t rank() const { return shape_.size(); }
     uint64_t numel() const { return numel_; }
@@ -89,8 +98,16 @@ class TensorObject {
 
     bool hostValid() const;
     bool deviceValid() const;
-    // The payload block, shared with views and with DLPack exports.
-    const std::shared_ptr<Storage> &storage() const { return storage_; }
+    // The payload block, shared with views and with DLPack exports (a
+    // transposed view is made contiguous first).
+    const std::shared_ptr<Storage> &storage() const;
+
+    // True while the payload is stored transposed ([dim1, dim0] row-major).
+    bool storedTransposed() const { return transposed_.load(std::memory_order_acquire); }
+    // The device payload as stored (uploading if needed), without making a
+    // transposed view contiguous; `keep` holds the block for the caller and
+    // `transposed` tells which layout the pointer has.
+    const void *storedDeviceData(std::shared_ptr<Storage> &keep, bool &transposed) const;
 
     // Element access with the reference's conversions (runtime.cpp:298-389).
     // A device-only tensor is not downloaded whole: one element is copied.
@@ -109,6 +126,9 @@ class TensorObject {
         : dtype_(dtype), shape_(std::move(shape)), numel_(numel), byteSize_(byteSize),
           storage_(std::move(storage)) {}
     void readElement(uint64_t flatIndex, void *dst) const;
+    // Replaces a transposed view's shared payload by a contiguous block of
+    // its own (no-op otherwise); thread-safe, runs at most once.
+    void makeContiguous() const;
     void printRecursive(std::ostream &os, size_t dimIndex, uint64_t &flatIndex,
                         const std::string &indent, const std::byte *data) const;
     std::string formatElement(const std::byte *data, uint64_t flatIndex) const;
@@ -117,7 +137,11 @@ class TensorObject {
     std::vector<int64_t> shape_;
     uint64_t numel_;
     size_t byteSize_;
-    std::shared_ptr<Storage> storage_;
+    // Replaced only by makeContiguous (under layoutMutex_), before which no
+    // accessor other than storedDeviceData reads it.
+    mutable std::shared_ptr<Storage> storage_;
+    mutable std::atomic<bool> transposed_{false};
+    mutable std::mutex layoutMutex_;
 };
 
 // modules/tensor/runtime.cpp:530-580

@@ -54,6 +54,12 @@ enum camel_hip_compare_op {
 
 /* Epilogue flags of the GEMM / conv entry points. */
 enum camel_hip_epilogue { CAMEL_EPI_NONE = 0, CAMEL_EPI_BIAS = 1, CAMEL_EPI_RELU = 2 };
+/* Operand layout flag of camel_hip_sgemm / camel_hip_sgemm_noalloc: A is given
+ * transposed, as At[K, M] row-major (A[m][k] = At[k][m]), and read in place by
+ * the MFMA tile loaders: transpose(X) @ E (test/run/nn/mnist.cml:39,
+ * test/run/nn/lr.cml:28; tensorTranspose2D runtime.cpp:704-720 followed by
+ * the matmul of operators.cpp:740-769) without a copy of X. */
+enum camel_hip_gemm_layout { CAMEL_GEMM_A_T = 0x10 };
 /* Layout bits of the conv2d flags, for a fused layer chain that keeps an
  * intermediate in the layout its consumer reads: x given as [N, H, W, C],
  * y written as [N, OH, OW, Co], w given as [Co, KH, KW, C] (packed once by
@@ -121,7 +127,9 @@ int camel_hip_arange(int64_t *out, int64_t start, int64_t step, int64_t count);
  * Replaces the ijk loop of __tensor_matmul__ (operators.cpp:740-769).
  * flags: CAMEL_EPI_BIAS adds bias[N] to every row (the ones@b broadcast idiom,
  * test/run/nn/mnist.cml:18, then add), CAMEL_EPI_RELU applies x*(x>0)
- * (test/run/nn/svm.cml:31), both fused in the GEMM epilogue. */
+ * (test/run/nn/svm.cml:31), both fused in the GEMM epilogue;
+ * CAMEL_GEMM_A_T: A given as At[K, M] (see camel_hip_gemm_layout).  Other
+ * flag bits are refused (CAMEL_HIP_ERR_ARG). */
 int camel_hip_sgemm(const float *A, const float *B, float *C, int64_t M, int64_t N, int64_t K,
                     const float *bias, int flags);
 /* Bytes of the static scratch of the allocation-free entry points (one copy

@@ -372,3 +372,22 @@ def test_noalloc_sgemm_refuses_before_initialisation():
     assert out.returncode == 0, out.stderr
     rc, msg = out.stdout.strip().split(" ", 1)
     assert int(rc) == H.ERR_ARG and "camel_hip_init" in msg
+
+
+def test_transpose_is_a_view_made_contiguous_on_read():
+    # Float32 transpose shares the payload (no copy at the call); reading it
+    # back makes it contiguous once, here on the host (the source never went
+    # to the device), and the values are the reference's transpose.
+    x = np.arange(12, dtype=np.float32).reshape(3, 4) * np.float32(0.5) - np.float32(2.0)
+    t = host(x)
+    tt = T.call("transpose", t)
+    assert tt.shape == (4, 3)
+    assert tt.residency() == (True, False)
+    np.testing.assert_array_equal(tt.numpy(), x.T)
+    # the transpose of a transposed view is the original layout again
+    np.testing.assert_array_equal(T.call("transpose", T.call("transpose", t)).numpy(), x)
+    # a reshape of a transposed view reads the transposed element order
+    r = T.call("reshape", T.call("transpose", t), [12])
+    np.testing.assert_array_equal(r.numpy(), x.T.reshape(12))
+    # indexing reads the logical layout
+    assert T.call("idx2d", T.call("transpose", t), 3, 1) == float(x[1, 3])
