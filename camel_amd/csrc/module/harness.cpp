@@ -252,6 +252,15 @@ int camel_tensor_format(uint64_t handle, char *buf, size_t cap, size_t *needed) 
     });
 }
 
+int camel_tensor_clone(uint64_t handle, uint64_t *copy) {
+    TensorObject *t = tensorOf(handle);
+    if (!t || !copy) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_clone: bad arguments");
+    return guarded([&] {
+        *copy = toSlot(t->clone());
+        return ok();
+    });
+}
+
 int camel_tensor_equals(uint64_t a, uint64_t b, int *equal) {
     TensorObject *ta = tensorOf(a), *tb = tensorOf(b);
     if (!ta || !tb || !equal) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_equals: bad arguments");

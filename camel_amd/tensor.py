@@ -87,6 +87,7 @@ _SIG = {
     "camel_tensor_live_count": ([], _I64),
     "camel_tensor_format": ([_U64, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)], C.c_int),
     "camel_tensor_equals": ([_U64, _U64, C.POINTER(C.c_int)], C.c_int),
+    "camel_tensor_clone": ([_U64, C.POINTER(_U64)], C.c_int),
     "camel_array_create": ([_U32, _I64, C.POINTER(_U64), C.POINTER(_U64)], C.c_int),
     "camel_array_read": ([_U64, C.POINTER(_U32), C.POINTER(_I64), C.POINTER(_U64), _I64], C.c_int),
     "camel_array_release": ([_U64], C.c_int),
@@ -225,6 +226,12 @@ class Tensor:
         eq = C.c_int()
         _check(load().camel_tensor_equals(self.handle, other.handle, C.byref(eq)))
         return bool(eq.value)
+
+    def clone(self) -> "Tensor":
+        """A deep copy with its own handle (TensorObject::clone)."""
+        h = _U64()
+        _check(load().camel_tensor_clone(self.handle, C.byref(h)))
+        return Tensor(h.value)
 
     def release(self) -> None:
         if self.handle:

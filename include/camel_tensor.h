@@ -83,6 +83,9 @@ int64_t camel_tensor_live_count(void);
 int camel_tensor_format(uint64_t handle, char *buf, size_t cap, size_t *needed);
 /* TensorObject::equals: same dtype, shape and bytes. */
 int camel_tensor_equals(uint64_t a, uint64_t b, int *equal);
+/* TensorObject::clone (runtime.cpp:407-417): a new handle with a deep copy of
+ * the payload (made on the device when the source has a device copy). */
+int camel_tensor_clone(uint64_t handle, uint64_t *copy);
 
 /* ---- DLPack (tensorToDLPackCopy / tensorFromDLPackCopy, runtime.cpp:1079-1124) */
 /* Exports a tensor as a DLManagedTensor; the consumer calls its deleter.

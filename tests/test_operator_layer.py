@@ -391,3 +391,14 @@ def test_transpose_is_a_view_made_contiguous_on_read():
     np.testing.assert_array_equal(r.numpy(), x.T.reshape(12))
     # indexing reads the logical layout
     assert T.call("idx2d", T.call("transpose", t), 3, 1) == float(x[1, 3])
+
+
+def test_clone_is_a_deep_copy_with_its_own_handle():
+    x = np.arange(6, dtype=np.float32).reshape(2, 3)
+    t = host(x)
+    c = t.clone()
+    assert c.handle != t.handle and c.equals(t)
+    t.release()
+    np.testing.assert_array_equal(c.numpy(), x)
+    with pytest.raises(T.CamelError):
+        T.Tensor(12345).clone()
