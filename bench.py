@@ -238,11 +238,11 @@ def wl_conv(steps, warmup):
 
 def wl_cnn(steps, warmup, fused=True):
     """Small CNN forward, batch 512 (valid 3x3 convs, 2x2 pool).
-    fused: conv1 writes NCHW4 for conv2 to read in place, conv2 + relu + pool
-    are one kernel (camel_hip_conv2d_pool2, weights packed once at setup),
-    and dense1 + relu + dense2 + softmax one head (camel_hip_dense_head: the
-    dense2 kernel adds dense1's split-K partials); otherwise every layer is
-    its own call."""
+    fused: conv1 + relu + conv2 + relu + pool are one kernel
+    (camel_hip_conv2d_pair_pool2: conv1's output stays in LDS; conv2's weights
+    packed once at setup), and dense1 + relu + dense2 + softmax one head
+    (camel_hip_dense_head: the dense2 kernel adds dense1's split-K partials);
+    otherwise every layer is its own call."""
     B = 512
     x = D.uniform(D.SEED_CNN, (B, 1, 28, 28), 0.0, 1.0)
     w1 = D.normal(D.SEED_CNN + 1, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
@@ -265,10 +265,8 @@ def wl_cnn(steps, warmup, fused=True):
 
     def step():
         if fused:
-            H.call("camel_hip_conv2d", P(dx.ptr), P(d1.ptr), P(b1.ptr), P(a1.ptr), B, 1, 28, 28, 32,
-                   3, 3, 1, 0, EPI | H.CONV_Y_NCHW4)
-            H.call("camel_hip_conv2d_pool2", P(a1.ptr), P(d2p.ptr), P(b2.ptr), P(a3.ptr), B, 32, 26,
-                   26, 64, 3, 3, 1, 0, EPI | H.CONV_X_NCHW4 | H.CONV_W_PACKED)
+            H.call("camel_hip_conv2d_pair_pool2", P(dx.ptr), P(d1.ptr), P(b1.ptr), P(d2p.ptr),
+                   P(b2.ptr), P(a3.ptr), B, 28, 28, 32, 64, EPI, EPI | H.CONV_W_PACKED)
             H.call("camel_hip_dense_head", P(a3.ptr), P(d3.ptr), P(b3.ptr), P(d4.ptr), P(b4.ptr),
                    P(dp.ptr), B, 9216, 128, 10, EPI, H.EPI_BIAS, 1)
             return

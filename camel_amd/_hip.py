@@ -67,6 +67,7 @@ _SIGNATURES = {
     "camel_hip_matmul_generic": [_I, _P, _I, _P, _I, _P, _I64, _I64, _I64],
     "camel_hip_conv2d": [_P, _P, _P, _P] + [_I64] * 9 + [_I],
     "camel_hip_conv2d_pool2": [_P, _P, _P, _P] + [_I64] * 9 + [_I],
+    "camel_hip_conv2d_pair_pool2": [_P] * 6 + [_I64] * 5 + [_I, _I],
     "camel_hip_conv2d_pack_weights": [_P, _P] + [_I64] * 4,
     "camel_hip_dense_softmax": [_P, _P, _P, _P, _I64, _I64, _I64, _I],
     "camel_hip_dense_head": [_P, _P, _P, _P, _P, _P] + [_I64] * 4 + [_I, _I, _I],

@@ -2100,6 +2100,202 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
     }
 }
 
+// ---- the first two convolutions of an image CNN, fused with the pool -----------
+//
+// y = maxpool2x2(conv2(conv1(x))) (each conv with its optional bias and relu)
+// for a one-channel input: conv1 1 -> CP_C1 channels, 3x3, then conv2
+// CP_C1 -> Co2, 3x3, both stride 1 and unpadded, then the 2x2 stride-2 pool.
+// conv1's output (CP_C1 x 26 x 26 per 28 x 28 image, 44 MB at batch 512)
+// never reaches HBM: a work-group computes the rows of it that its band of
+// conv2 rows reads into LDS, then runs conv2 as an implicit GEMM whose B
+// operand is read straight from that LDS patch, and stores only the pooled
+// values.
+//   * work-group = (image, band of CP_BR pooled rows = 2 CP_BR conv2 rows) x
+//     64 output channels; 4 waves as 2 (channels) x 2 (column halves), each
+//     wave 32 channels x CP_NBW blocks of 32 columns;
+//   * columns in pool order, 4 per window ((0,0), (0,1), (1,0), (1,1)), so a
+//     window is one DPP quad and the epilogue takes its max in registers;
+//   * conv1 is the direct kernel's FMA chain (k = (kh, kw) ascending, then
+//     bias and x * (x > 0)), so the patch holds exactly the values the conv1
+//     kernel stores;
+//   * conv2's A operand (weights packed [Co2][3][3][CP_C1]) is held in
+//     registers for all of K; the MFMA sequence -- K in (kh, kw, c) order,
+//     8-channel groups, each 32x32x2 MFMA pairing channels c and c + 4 --
+//     and the epilogue (bias, relu, strict-'>' window max) are those of the
+//     implicit GEMM with the pooled NCHW4 loader, so the result equals the
+//     two conv calls and the pool bit for bit.
+constexpr int CP_C1 = 32;                 // conv1 output channels = conv2 input channels
+constexpr int CP_W = 28;                  // input width
+constexpr int CP_OW1 = CP_W - 2;          // conv1 output width (26)
+constexpr int CP_PW = (CP_OW1 - 2) / 2;   // pooled width (12)
+constexpr int CP_BR = 4;                  // pooled rows per work-group
+constexpr int CP_R1 = 2 * CP_BR + 2;      // conv1 rows a band reads (10)
+constexpr int CP_IR = CP_R1 + 2;          // input rows a band reads (12)
+// The patch is stored by channel quads, [C1/4][CP_R1][CP_RS][4]: a lane reads
+// the 4 channels of one pixel that 4 consecutive MFMAs take with one 16-byte
+// read, and with a row pitch of CP_RS = 28 (= 4 mod 8) pixels, the 8 lanes a
+// 16-byte read serves at a time (2 windows: 2 x 4 pixels over 2 or 4 rows)
+// fall on 8 distinct bank groups.
+constexpr int CP_RS = 28;
+static_assert(CP_RS >= CP_OW1 && CP_RS % 8 == 4, "conflict-free patch row pitch");
+constexpr int CP_QPLANE = CP_R1 * CP_RS * 4; // one channel quad of the patch (1120 floats)
+constexpr int CP_COLS = CP_BR * CP_PW * 4; // GEMM columns of a band (192)
+constexpr int CP_NBW = CP_COLS / 32 / 2;  // 32-column blocks per wave (3)
+static_assert(CP_COLS % 64 == 0, "a band is whole 32-column blocks for both column halves");
+
+__global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
+    const float *__restrict__ x, const float *__restrict__ w1, const float *__restrict__ b1,
+    const float *__restrict__ w2p, const float *__restrict__ b2, float *__restrict__ y, int H,
+    int Co2, int bands, int flags1, int flags2) {
+    const bool BIAS1 = flags1 & CAMEL_EPI_BIAS, RELU1 = flags1 & CAMEL_EPI_RELU;
+    const bool BIAS2 = flags2 & CAMEL_EPI_BIAS, RELU2 = flags2 & CAMEL_EPI_RELU;
+    __shared__ __attribute__((aligned(16))) float patch[CP_C1 / 4 * CP_QPLANE];
+    __shared__ float img[CP_IR * CP_W];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = lane >> 5, r32 = lane & 31;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int n = blockIdx.x / bands, band = blockIdx.x - n * bands;
+    const int m0 = blockIdx.y * 64;
+    const int PH = bands * CP_BR;
+    const int Y0 = band * 2 * CP_BR; // first conv2 (and conv1) row of the band
+
+    // conv2 weights of this lane's row as the MFMA A operand, one (kh, kw)
+    // at a time: a[buf][s8] holds channels 8 s8 + 4 half .. +3 (from L2,
+    // two (kh, kw) ahead of their use).
+    const float *wr = w2p + (size_t)(m0 + 32 * wm + r32) * 9 * CP_C1 + 4 * half;
+    float4 a[3][CP_C1 / 8];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int s8 = 0; s8 < CP_C1 / 8; ++s8)
+            a[j][s8] = *reinterpret_cast<const float4 *>(wr + j * CP_C1 + 8 * s8);
+
+    // The input rows of the band (zeros past the image: never read by a
+    // valid output, since the bands tile the pooled rows exactly).
+    const float *xi = x + (size_t)n * H * CP_W;
+    for (int i = tid; i < CP_IR * CP_W; i += 256) {
+        const int r = Y0 + i / CP_W;
+        img[i] = r < H ? xi[(size_t)Y0 * CP_W + i] : 0.f;
+    }
+    __syncthreads();
+
+    // conv1 into the patch: one pixel per thread, all channels; weights and
+    // bias are wave-uniform (scalar loads).
+    for (int p = tid; p < CP_R1 * CP_OW1; p += 256) {
+        const int r = p / CP_OW1, c = p - r * CP_OW1;
+        float xv[9];
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) xv[kh * 3 + kw] = img[(r + kh) * CP_W + c + kw];
+        float *dst = patch + (r * CP_RS + c) * 4;
+#pragma unroll 2
+        for (int cq = 0; cq < CP_C1 / 4; ++cq) {
+            float4 q;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int ch = 4 * cq + u;
+                float acc = 0.f;
+#pragma unroll
+                for (int k = 0; k < 9; ++k) acc = __builtin_fmaf(w1[ch * 9 + k], xv[k], acc);
+                if (BIAS1) acc = acc + b1[ch];
+                if (RELU1) acc = relu_idiom(acc);
+                q[u] = acc;
+            }
+            *reinterpret_cast<float4 *>(dst + cq * CP_QPLANE) = q;
+        }
+    }
+    __syncthreads();
+
+    // conv2: lane (r32, half) reads B[k][col] for channels 8 s8 + 4 half + t,
+    // t = 0..3, of pixel (oy + kh, ox + kw) of its column col of each block:
+    // one 16-byte read of channel quad 2 s8 + half.
+    int base[CP_NBW];
+#pragma unroll
+    for (int b = 0; b < CP_NBW; ++b) {
+        const int col = 32 * (CP_NBW * wn + b) + r32;
+        const int win = col >> 2, d = col & 3;
+        const int py = win / CP_PW, px = win - py * CP_PW;
+        base[b] = half * CP_QPLANE + ((2 * py + (d >> 1)) * CP_RS + 2 * px + (d & 1)) * 4;
+    }
+    floatx16 acc[CP_NBW];
+#pragma unroll
+    for (int b = 0; b < CP_NBW; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
+    // Each (kh, kw) stage issues the weight loads of stage + 2 first; within
+    // a stage the patch reads of the next 8-channel group go out before the
+    // current group's MFMAs (scheduling barriers keep that order).
+    auto patch_reads = [&](int khw, int s8, float4 *bv) {
+        const int kh = khw / 3, kw = khw - 3 * (khw / 3);
+        const int off = 2 * s8 * CP_QPLANE + (kh * CP_RS + kw) * 4;
+#pragma unroll
+        for (int b = 0; b < CP_NBW; ++b)
+            bv[b] = *reinterpret_cast<const float4 *>(patch + base[b] + off);
+    };
+    float4 bv[2][CP_NBW];
+    patch_reads(0, 0, bv[0]);
+#pragma unroll
+    for (int khw = 0; khw < 9; ++khw) {
+        const int cur = khw % 3;
+        if (khw + 2 < 9) {
+#pragma unroll
+            for (int s8 = 0; s8 < CP_C1 / 8; ++s8)
+                a[(khw + 2) % 3][s8] =
+                    *reinterpret_cast<const float4 *>(wr + (khw + 2) * CP_C1 + 8 * s8);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s8 = 0; s8 < CP_C1 / 8; ++s8) {
+            const int g = khw * (CP_C1 / 8) + s8; // group index over all of K
+            if (g + 1 < 9 * (CP_C1 / 8))
+                patch_reads((g + 1) / (CP_C1 / 8), (g + 1) % (CP_C1 / 8), bv[(g + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int b = 0; b < CP_NBW; ++b)
+                    acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][s8][t], bv[g & 1][b][t],
+                                                                  acc[b], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // Epilogue: bias, relu, then the window max over the lane quad in the
+    // order (0,0), (0,1), (1,0), (1,1) with a strict '>'; the quad's first
+    // lane stores the pooled value.
+    float brow[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        brow[v] = BIAS2 ? b2[m0 + 32 * wm + 8 * (v >> 2) + 4 * half + (v & 3)] : 0.f;
+#pragma unroll
+    for (int b = 0; b < CP_NBW; ++b) {
+        const int col = 32 * (CP_NBW * wn + b) + r32;
+        const int win = col >> 2;
+        const int py = band * CP_BR + win / CP_PW, px = win % CP_PW;
+        float *out = y + ((size_t)n * Co2 + m0 + 32 * wm) * PH * CP_PW + (size_t)py * CP_PW + px;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = 8 * (v >> 2) + 4 * half + (v & 3);
+            float xo = acc[b][v];
+            if (BIAS2) xo = xo + brow[v];
+            if (RELU2) xo = relu_idiom(xo);
+            const float x1 = quad_lane<1>(xo), x2 = quad_lane<2>(xo), x3 = quad_lane<3>(xo);
+            float mx = xo;
+            if (x1 > mx) mx = x1;
+            if (x2 > mx) mx = x2;
+            if (x3 > mx) mx = x3;
+            if ((r32 & 3) == 0) out[(size_t)row * PH * CP_PW] = mx;
+        }
+    }
+}
+
+// True when conv_pair_pool_kernel serves the pair.
+bool conv_pair_supported(int64_t H, int64_t W, int64_t C1, int64_t Co2) {
+    return W == CP_W && C1 == CP_C1 && Co2 > 0 && Co2 % 64 == 0 && H >= 6 &&
+           (H - 4) % (2 * CP_BR) == 0;
+}
+
 // ---- conv2d host paths -----------------------------------------------------------
 
 // Activation layouts of the conv paths: NCHW (the tensor layout), NHWC and
@@ -2745,6 +2941,44 @@ int camel_hip_conv2d_pack_weights(const float *w, float *wp, int64_t Co, int64_t
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
     CAMEL_RETURN_IF(pack_weights(w, wp, Co, C, KH * KW));
+    return ok();
+}
+
+int camel_hip_conv2d_pair_pool2(const float *x, const float *w1, const float *b1, const float *w2,
+                                const float *b2, float *y, int64_t N, int64_t H, int64_t W,
+                                int64_t C1, int64_t Co2, int flags1, int flags2) {
+    const char *who = "conv2d_pair_pool2";
+    if (N < 0 || H <= 0 || W <= 0 || C1 <= 0 || Co2 <= 0)
+        return fail(CAMEL_HIP_ERR_SHAPE, std::string(who) + ": invalid geometry");
+    if ((flags1 & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU)) ||
+        (flags2 & ~(CAMEL_EPI_BIAS | CAMEL_EPI_RELU | CAMEL_CONV_W_PACKED)))
+        return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": unknown flags");
+    if (!conv_pair_supported(H, W, C1, Co2) || N > INT32_MAX / 64 ||
+        !product_fits({N, Co2, (H - 4) / 2, (W - 4) / 2}))
+        return fail(CAMEL_HIP_ERR_SHAPE,
+                    std::string(who) + ": shape not served (needs W = 28, C1 = 32, Co2 % 64 == 0, "
+                                       "(H - 4) % 8 == 0)");
+    if (((flags1 & CAMEL_EPI_BIAS) && !b1) || ((flags2 & CAMEL_EPI_BIAS) && !b2))
+        return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": null bias");
+    if (N == 0) return ok();
+    if (!x || !w1 || !w2 || !y) return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": null operand");
+    if (((uintptr_t)w2 & 15) != 0) return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": w2 not 16-byte aligned");
+    CAMEL_LOCK();
+    CAMEL_INIT_OR_RETURN();
+    const float *w2p = w2;
+    Scratch packed;
+    if (!(flags2 & CAMEL_CONV_W_PACKED)) {
+        CAMEL_RETURN_IF(packed.alloc((size_t)Co2 * C1 * 9 * sizeof(float)));
+        CAMEL_RETURN_IF(pack_weights(w2, packed.f(), Co2, C1, 9));
+        w2p = packed.f();
+    }
+    const int bands = (int)((H - 4) / 2 / CP_BR);
+    const dim3 grid((unsigned)(N * bands), (unsigned)(Co2 / 64));
+    hipLaunchKernelGGL(conv_pair_pool_kernel, grid, dim3(256), 0, stream(), x, w1, b1, w2p, b2, y,
+                       (int)H, (int)Co2, bands, flags1 & (CAMEL_EPI_BIAS | CAMEL_EPI_RELU),
+                       flags2 & (CAMEL_EPI_BIAS | CAMEL_EPI_RELU));
+    const int rc = check_launch("conv_pair_pool_kernel");
+    CAMEL_RETURN_IF(rc);
     return ok();
 }
 

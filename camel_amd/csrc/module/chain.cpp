@@ -29,6 +29,23 @@ int64_t intOr(const LayerStep &s, size_t i, int64_t fallback) {
     return i < s.ints.size() ? s.ints[i] : fallback;
 }
 
+bool isF32(const TensorObject *t) { return !t || t->dtype() == TypeCode::Float32; }
+
+// The shapes camel_hip_conv2d_pair_pool2 serves: x [N, 1, H, 28] Float32,
+// conv1 32 x 1 x 3 x 3 and conv2 Co x 32 x 3 x 3 (Co % 64 == 0), both
+// stride 1, unpadded, with [Co] biases, and (H - 4) % 8 == 0.
+bool pairServes(std::span<const int64_t> xs, TypeCode xdt, const LayerStep &c1,
+                const LayerStep &c2) {
+    auto conv3 = [](const LayerStep &c, int64_t cin) {
+        return c.w->rank() == 4 && c.w->dim(1) == cin && c.w->dim(2) == 3 && c.w->dim(3) == 3 &&
+               intOr(c, 0, 1) == 1 && intOr(c, 1, 0) == 0 && isF32(c.w) && isF32(c.bias) &&
+               (!c.bias || (c.bias->rank() == 1 && c.bias->dim(0) == c.w->dim(0)));
+    };
+    return xs.size() == 4 && xdt == TypeCode::Float32 && xs[1] == 1 && xs[3] == 28 && xs[2] >= 6 &&
+           (xs[2] - 4) % 8 == 0 && conv3(c1, 1) && c1.w->dim(0) == 32 && conv3(c2, 32) &&
+           c2.w->dim(0) % 64 == 0;
+}
+
 // A device activation between two groups: a tensor, or an NCHW4 buffer
 // ([N][C/4][H][W][4]) of the logical NCHW shape `shape` that only a conv
 // reads.
@@ -138,7 +155,8 @@ const void *LayerChain::packedWeights(size_t i) const {
     return packed_[i];
 }
 
-std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> shape) const {
+std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> shape,
+                                                    TypeCode dtype) const {
     std::vector<Group> groups;
     // Batch of the current activation where it is known (rank-4 shapes are
     // propagated through conv / pool / relu; anything else stops NCHW4
@@ -185,6 +203,27 @@ std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> sha
             if (!g.relu && j < n && steps_[j].kind == LayerKind::Relu) {
                 g.relu = true;
                 ++j;
+            }
+            if (groups.empty() && j < n && steps_[j].kind == LayerKind::Conv2d &&
+                pairServes(shape, dtype, s, steps_[j])) {
+                // conv2d (relu) conv2d (relu) maxpool2d(2, 2) at the chain's
+                // start: one kernel, the first conv's output kept in LDS
+                size_t k = j + 1;
+                bool relu2 = steps_[j].relu;
+                if (!relu2 && k < n && steps_[k].kind == LayerKind::Relu) {
+                    relu2 = true;
+                    ++k;
+                }
+                if (k < n && steps_[k].kind == LayerKind::MaxPool2d && intOr(steps_[k], 0, 2) == 2 &&
+                    intOr(steps_[k], 1, intOr(steps_[k], 0, 2)) == 2) {
+                    g.kind = Group::ConvPair;
+                    g.step2 = &steps_[j];
+                    g.relu2 = relu2;
+                    g.pool = true;
+                    groups.push_back(g);
+                    i = k + 1;
+                    continue;
+                }
             }
             if (j < n && steps_[j].kind == LayerKind::MaxPool2d && intOr(steps_[j], 0, 2) == 2 &&
                 intOr(steps_[j], 1, intOr(steps_[j], 0, 2)) == 2) {
@@ -233,6 +272,10 @@ std::string LayerChain::plan(std::span<const int64_t> shape) const {
             out << (g.relu ? "dense_relu+" : "dense+") << (g.relu2 ? "dense_relu" : "dense");
             if (g.softmax) out << "+softmax";
             break;
+        case Group::ConvPair:
+            out << (g.relu ? "conv2d_relu+" : "conv2d+") << (g.relu2 ? "conv2d_relu" : "conv2d")
+                << "+maxpool2d(2,2)";
+            break;
         case Group::Conv:
             out << (g.relu ? "conv2d_relu" : "conv2d");
             if (g.pool) out << "+maxpool2d(2,2)";
@@ -267,10 +310,33 @@ TensorObject *LayerChain::apply(const TensorObject *x) const {
     Activation cur;
     cur.tensor = x;
     cur.shape.assign(x->shape(), x->shape() + x->rank());
-    for (const Group &g : schedule(cur.shape)) {
+    for (const Group &g : schedule(cur.shape, cur.tensor->dtype())) {
         const LayerStep &s = *g.step;
         Activation next;
         switch (g.kind) {
+        case Group::ConvPair: {
+            // schedule() checked every shape and dtype this kernel needs
+            const LayerStep &s2 = *g.step2;
+            const int64_t N = cur.shape[0], H = cur.shape[2], W = cur.shape[3];
+            const int64_t Co2 = s2.w->dim(0);
+            const int64_t os[4] = {N, Co2, (H - 4) / 2, (W - 4) / 2};
+            next = Activation::of(TensorObject::create(TypeCode::Float32, os, Residence::Device));
+            if (N > 0) {
+                const int f1 = (s.bias ? CAMEL_EPI_BIAS : 0) | (g.relu ? CAMEL_EPI_RELU : 0);
+                const int f2 = (s2.bias ? CAMEL_EPI_BIAS : 0) | (g.relu2 ? CAMEL_EPI_RELU : 0) |
+                               CAMEL_CONV_W_PACKED;
+                const void *w2p = packedWeights((size_t)(&s2 - steps_.data()));
+                checkHip(camel_hip_conv2d_pair_pool2(
+                    static_cast<const float *>(cur.tensor->deviceData()),
+                    static_cast<const float *>(s.w->deviceData()),
+                    s.bias ? static_cast<const float *>(s.bias->deviceData()) : nullptr,
+                    static_cast<const float *>(w2p),
+                    s2.bias ? static_cast<const float *>(s2.bias->deviceData()) : nullptr,
+                    static_cast<float *>(const_cast<TensorObject *>(next.tensor)->deviceOutput()),
+                    N, H, W, 32, Co2, f1, f2));
+            }
+            break;
+        }
         case Group::Dense:
             next = Activation::of(tensorDense(cur.tensor, s.w, s.bias, g.relu));
             break;

@@ -13,6 +13,9 @@
 //                                        layer's kernel adds the first
 //                                        one's split-K partials)
 //   conv2d (+relu) + maxpool2d(2, 2)  -> camel_hip_conv2d_pool2
+//   conv2d 1->32 3x3 (+relu) + conv2d 32->Co 3x3 (+relu) + maxpool2d(2, 2)
+//     on 28-wide images               -> camel_hip_conv2d_pair_pool2 (the
+//                                        first conv's output stays in LDS)
 //   conv2d -> conv2d that reads NCHW4 -> the first writes NCHW4
 //                                        ([N][C/4][H][W][4]) and the second
 //                                        reads it in place (no transpose)
@@ -70,18 +73,19 @@ public:
 
 private:
     struct Group {
-        enum Kind { Dense, DenseSoftmax, DenseHead, Conv, Relu, Softmax, MaxPool, Reshape } kind;
+        enum Kind { Dense, DenseSoftmax, DenseHead, Conv, ConvPair, Relu, Softmax, MaxPool, Reshape } kind;
         const LayerStep *step; // first layer of the group
-        const LayerStep *step2 = nullptr; // DenseHead: the second dense
+        const LayerStep *step2 = nullptr; // DenseHead / ConvPair: the second dense / conv
         bool relu = false;
-        bool relu2 = false;    // DenseHead: relu after the second dense
+        bool relu2 = false;    // DenseHead / ConvPair: relu after the second layer
         bool softmax = false;  // DenseHead: row softmax at the end
         bool pool = false;     // conv + maxpool2d(2, 2)
         bool x_nchw4 = false;  // conv input comes NCHW4 from the previous conv
         bool y_nchw4 = false;  // conv output goes NCHW4 to the next conv
         bool w_packed = false; // conv runs as the implicit GEMM: weights packed once
     };
-    std::vector<Group> schedule(std::span<const int64_t> shape) const;
+    std::vector<Group> schedule(std::span<const int64_t> shape,
+                                TypeCode dtype = TypeCode::Float32) const;
     // The packed form of step i's conv weights (made on first use; tensors
     // never change once made, so it stays valid while the chain lives).
     const void *packedWeights(size_t i) const;

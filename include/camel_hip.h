@@ -201,6 +201,22 @@ int camel_hip_conv2d_pack_weights(const float *w, float *wp, int64_t Co, int64_t
 int camel_hip_conv2d_pool2(const float *x, const float *w, const float *bias, float *y, int64_t N,
                            int64_t C, int64_t H, int64_t W, int64_t Co, int64_t KH, int64_t KW,
                            int64_t stride, int64_t pad, int flags);
+/* y[N,Co2,(H-4)/2,(W-4)/2] = maxpool2x2(conv2(conv1(x))): the
+ * conv2d..conv2d..maxpool2d(2, 2) opening of an image CNN
+ * (`conv2d<w1,b1>..relu..conv2d<w2,b2>..relu..maxpool2d`) in one kernel, with
+ * conv1 = x[N,1,H,W] * w1[C1,1,3,3] (+b1) (relu) and conv2 = conv1 *
+ * w2[Co2,C1,3,3] (+b2) (relu), both stride 1 and unpadded; flags1 / flags2
+ * carry each conv's CAMEL_EPI_* bits, flags2 may add CAMEL_CONV_W_PACKED (w2
+ * as [Co2,3,3,C1]).  conv1's output never reaches HBM: each work-group
+ * computes the rows its band of conv2 reads into LDS.  Equals
+ * camel_hip_conv2d(conv1, CAMEL_CONV_Y_NCHW4) followed by
+ * camel_hip_conv2d_pool2(conv2, CAMEL_CONV_X_NCHW4) bit for bit.  Served
+ * shapes: W = 28, C1 = 32, Co2 % 64 == 0, (H - 4) % 8 == 0 (MNIST-style
+ * 28 x 28 inputs); others return CAMEL_HIP_ERR_SHAPE.  No reference operator:
+ * the reference's compose is a stub (src/builtin/operators/macro.cpp:30). */
+int camel_hip_conv2d_pair_pool2(const float *x, const float *w1, const float *b1, const float *w2,
+                                const float *b2, float *y, int64_t N, int64_t H, int64_t W,
+                                int64_t C1, int64_t Co2, int flags1, int flags2);
 /* Max pool, NCHW, window KH x KW, first-then-strict-'>' rule of tensorMaxAxis
  * (runtime.cpp:953-958).  OH = (H-KH)/stride+1. */
 int camel_hip_maxpool2d(const float *x, float *y, int64_t N, int64_t C, int64_t H, int64_t W,

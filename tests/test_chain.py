@@ -28,11 +28,24 @@ def cnn_chain(c1=1, c2=32, c3=64):
 
 
 def test_cnn_chain_plan_fuses_every_pair():
-    # The benchmark small CNN as a chain: conv1 writes NCHW4 for conv2, conv2 + relu
-    # + pool are one kernel, and the two dense layers with the softmax one head.
+    # The benchmark small CNN as a chain: both convs, their relus and the pool
+    # are one kernel (conv1's output stays in LDS), and the two dense layers
+    # with the softmax one head.
     assert cnn_chain().plan((512, 1, 28, 28)) == [
-        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4", "reshape",
-        "dense_relu+dense+softmax"]
+        "conv2d_relu+conv2d_relu+maxpool2d(2,2)", "reshape", "dense_relu+dense+softmax"]
+    # Shapes the fused pair does not serve keep the NCHW4 hand-off: a 32-wide
+    # image, 16 conv1 channels, or 96 conv2 channels.
+    assert T.Chain(("conv2d", z(32, 1, 3, 3), z(32)), "relu",
+                   ("conv2d_relu", z(64, 32, 3, 3), z(64)), ("maxpool2d", 2, 2)).plan(
+        (8, 1, 28, 32)) == ["conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4"]
+    assert cnn_chain(c2=16, c3=64).plan((8, 1, 28, 28))[:2] == [
+        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4"]
+    assert T.Chain(("conv2d_relu", z(32, 1, 3, 3)), ("conv2d_relu", z(96, 32, 3, 3)),
+                   ("maxpool2d", 2, 2)).plan((8, 1, 28, 28)) == [
+        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4"]
+    # without the pool the pair is not fused either
+    assert T.Chain(("conv2d_relu", z(32, 1, 3, 3)), ("conv2d_relu", z(64, 32, 3, 3))).plan(
+        (8, 1, 28, 28)) == ["conv2d_relu y=nchw4", "conv2d_relu x=nchw4"]
 
 
 def test_mlp_chain_plan():

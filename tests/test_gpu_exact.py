@@ -276,6 +276,21 @@ def test_cnn_pooled_conv2_from_nchw4_is_exact():
     assert_bits(_conv(x, wp, b, geom, flags, pooled=True, x_layout="nchw4"), want, "pooled conv2")
 
 
+def test_conv_pair_pool_kernel_is_exact():
+    # camel_hip_conv2d_pair_pool2 at BASELINE config 5's shape: conv1 into LDS,
+    # conv2 from it, the 2x2 pool, against the exact result.
+    x = ints(0x7150, (512, 1, 28, 28), 0, 1)
+    w1, b1 = ints(0x7151, (32, 1, 3, 3), -1, 1), ints(0x7152, (32,), -1, 1)
+    w2, b2 = ints(0x7153, (64, 32, 3, 3), -1, 1), ints(0x7154, (64,), -1, 1)
+    want = pool2(exact_conv(exact_conv(x, w1, b1, relu=True), w2, b2, relu=True))
+    dx, dw1, db1, dw2, db2 = K.dev(x), K.dev(w1), K.dev(b1), K.dev(w2), K.dev(b2)
+    dy = K.empty(want.nbytes)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    H.call("camel_hip_conv2d_pair_pool2", P(dx.ptr), P(dw1.ptr), P(db1.ptr), P(dw2.ptr),
+           P(db2.ptr), P(dy.ptr), 512, 28, 28, 32, 64, epi, epi)
+    assert_bits(K.host(dy, F, want.shape), want, "conv pair + pool")
+
+
 # ------------------------------------------------------------- layer chains
 
 @pytest.fixture
@@ -311,8 +326,8 @@ def test_mlp_chain_full_batch_is_exact(_release):
 
 def test_cnn_chain_full_batch_is_exact(_release):
     # BASELINE config 5's shapes at batch 512 through the fused chain (conv1
-    # direct -> NCHW4 -> pooled conv2 -> dense head on split partials): the
-    # logits exactly, then the softmax within its bar, for all 512 images.
+    # into LDS -> conv2 -> pool in one kernel, dense head on split partials):
+    # the logits exactly, then the softmax within its bar, for all 512 images.
     x = ints(0x7300, (512, 1, 28, 28), 0, 1)
     w1, b1 = ints(0x7301, (32, 1, 3, 3), -1, 1), ints(0x7302, (32,), -1, 1)
     w2, b2 = ints(0x7303, (64, 32, 3, 3), -1, 1), ints(0x7304, (64,), -1, 1)
@@ -326,8 +341,8 @@ def test_cnn_chain_full_batch_is_exact(_release):
     layers = [("conv2d_relu", tw[0], tw[1]), ("conv2d_relu", tw[2], tw[3]), ("maxpool2d", 2, 2),
               ("reshape", 512, 9216), ("dense_relu", tw[4], tw[5]), ("dense", tw[6], tw[7])]
     head = T.Chain(*layers)
-    assert head.plan((512, 1, 28, 28))[:2] == ["conv2d_relu y=nchw4",
-                                               "conv2d_relu+maxpool2d(2,2) x=nchw4"]
+    assert head.plan((512, 1, 28, 28))[:2] == ["conv2d_relu+conv2d_relu+maxpool2d(2,2)",
+                                               "reshape"]
     assert_bits(head(t(x)).numpy(), logits, "CNN logits")
     full = T.Chain(*layers, "softmax")
     softmax_close(full(t(x)).numpy(), logits)

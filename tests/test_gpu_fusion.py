@@ -462,3 +462,60 @@ def test_conv2d_packed_weights_change_addressing_only(geom):
         dpool, pshape = _conv(x, w, b, geom, epi, pooled=True)
         dy, _ = _conv(x, wp, b, geom, epi | H.CONV_W_PACKED, pooled=True)
         np.testing.assert_array_equal(K.host(dy, F, pshape), K.host(dpool, F, pshape))
+
+
+# ------------------------------------------- conv2d..conv2d..maxpool2d in one kernel
+
+def _pair_unfused(x, w1, b1, w2, b2, f1, f2):
+    N, _, H_, W_ = x.shape
+    C1, Co2 = w1.shape[0], w2.shape[0]
+    dx, dw1, dw2 = K.dev(x), K.dev(w1), K.dev(w2)
+    db1 = K.dev(b1) if b1 is not None else None
+    db2 = K.dev(b2) if b2 is not None else None
+    h = K.empty(N * C1 * (H_ - 2) * (W_ - 2) * 4)
+    H.call("camel_hip_conv2d", P(dx.ptr), P(dw1.ptr), P(db1.ptr) if db1 else None, P(h.ptr), N, 1,
+           H_, W_, C1, 3, 3, 1, 0, f1 | H.CONV_Y_NCHW4)
+    OH, OW = (H_ - 4) // 2, (W_ - 4) // 2
+    y = K.empty(N * Co2 * OH * OW * 4)
+    H.call("camel_hip_conv2d_pool2", P(h.ptr), P(dw2.ptr), P(db2.ptr) if db2 else None, P(y.ptr),
+           N, C1, H_ - 2, W_ - 2, Co2, 3, 3, 1, 0, f2 | H.CONV_X_NCHW4)
+    return K.host(y, F, (N, Co2, OH, OW))
+
+
+def _pair_fused(x, w1, b1, w2, b2, f1, f2, packed=False):
+    N, _, H_, W_ = x.shape
+    C1, Co2 = w1.shape[0], w2.shape[0]
+    w2x = np.ascontiguousarray(w2.transpose(0, 2, 3, 1)) if packed else w2
+    dx, dw1, dw2 = K.dev(x), K.dev(w1), K.dev(w2x)
+    db1 = K.dev(b1) if b1 is not None else None
+    db2 = K.dev(b2) if b2 is not None else None
+    OH, OW = (H_ - 4) // 2, (W_ - 4) // 2
+    y = K.empty(N * Co2 * OH * OW * 4)
+    H.call("camel_hip_conv2d_pair_pool2", P(dx.ptr), P(dw1.ptr), P(db1.ptr) if db1 else None,
+           P(dw2.ptr), P(db2.ptr) if db2 else None, P(y.ptr), N, H_, W_, C1, Co2, f1,
+           f2 | (H.CONV_W_PACKED if packed else 0))
+    return K.host(y, F, (N, Co2, OH, OW))
+
+
+@pytest.mark.parametrize("N,H_,Co2,f1,f2", [
+    (512, 28, 64, H.EPI_BIAS | H.EPI_RELU, H.EPI_BIAS | H.EPI_RELU),
+    (3, 28, 64, H.EPI_RELU, H.EPI_RELU),
+    (7, 36, 128, H.EPI_BIAS | H.EPI_RELU, H.EPI_BIAS),                  # taller images, 2 M tiles
+    (2, 12, 64, 0, 0),
+])
+def test_conv_pair_pool_equals_the_two_conv_calls(N, H_, Co2, f1, f2):
+    x = D.uniform(0x5B00 + N, (N, 1, H_, 28), 0.0, 1.0)
+    w1 = D.normal(0x5B01, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9)))
+    w2 = D.normal(0x5B02 + Co2, (Co2, 32, 3, 3), std=float(np.sqrt(2.0 / 288)))
+    b1 = D.uniform(0x5B03, (32,), -0.1, 0.1)
+    b2 = D.uniform(0x5B04, (Co2,), -0.1, 0.1)
+    bb1 = b1 if f1 & H.EPI_BIAS else None
+    bb2 = b2 if f2 & H.EPI_BIAS else None
+    want = _pair_unfused(x, w1, bb1, w2, bb2, f1, f2)
+    for packed in (False, True):
+        got = _pair_fused(x, w1, bb1, w2, bb2, f1, f2, packed)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"packed={packed}"
+    # and the oracle on the first image
+    h = O.conv2d_images(x, w1, bb1, bool(f1 & H.EPI_RELU), 0, 1)
+    ref = O.maxpool2d(O.conv2d(h, w2, bb2, bool(f2 & H.EPI_RELU)), 2, 2)
+    assert np.max(np.abs(got[:1] - ref)) <= 1e-4 * max(1.0, float(np.abs(ref).max()))

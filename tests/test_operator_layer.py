@@ -7,6 +7,7 @@ shape errors the reference raises before touching data are raised with the
 same text.  Host tensors stay on the host until a device operator needs them,
 so these error paths never reach libcamel_hip's device code.
 """
+import ctypes as C
 import os
 import re
 
@@ -79,6 +80,20 @@ def test_hip_abi_rejects_extents_whose_products_overflow():
     assert gm(H.DT_I64, None, H.DT_I64, None, H.DT_I64, None, 2**60, 1, 4) == H.ERR_SHAPE
     assert gm(H.DT_BOOL, None, H.DT_BOOL, None, H.DT_BOOL, None, 4, 2**61, 1) == H.ERR_SHAPE
     assert b"too large" in lib.camel_hip_last_error()
+
+
+def test_conv_pair_pool_refuses_shapes_it_does_not_serve():
+    # Checked before any device work: the pointers are never dereferenced.
+    lib = H.load()
+    p = [C.c_void_p(256)] * 6
+    pair = lib.camel_hip_conv2d_pair_pool2
+    assert pair(*p, 2, 28, 30, 32, 64, 0, 0) == H.ERR_SHAPE     # W != 28
+    assert pair(*p, 2, 28, 28, 16, 64, 0, 0) == H.ERR_SHAPE     # C1 != 32
+    assert pair(*p, 2, 28, 28, 32, 32, 0, 0) == H.ERR_SHAPE     # Co2 % 64 != 0
+    assert pair(*p, 2, 26, 28, 32, 64, 0, 0) == H.ERR_SHAPE     # (H - 4) % 8 != 0
+    assert b"shape not served" in lib.camel_hip_last_error()
+    assert pair(*p, 2, 28, 28, 32, 64, 0x400, 0) == H.ERR_ARG   # packing is conv2's flag
+    assert pair(*p, -1, 28, 28, 32, 64, 0, 0) == H.ERR_SHAPE
 
 
 def test_tensor_abi_exports_every_declared_symbol():
