@@ -2138,7 +2138,10 @@ constexpr int CP_IR = CP_R1 + 2;          // input rows a band reads (12)
 // fall on 8 distinct bank groups.
 constexpr int CP_RS = 28;
 static_assert(CP_RS >= CP_OW1 && CP_RS % 8 == 4, "conflict-free patch row pitch");
-constexpr int CP_QPLANE = CP_R1 * CP_RS * 4; // one channel quad of the patch (1120 floats)
+// One channel quad of the patch: 1120 floats, padded to 1124 (= 4 mod 32) so
+// that the conv1 phase's 32 lanes, one channel each, store one pixel to 32
+// distinct banks.
+constexpr int CP_QPLANE = CP_R1 * CP_RS * 4 + 4;
 constexpr int CP_COLS = CP_BR * CP_PW * 4; // GEMM columns of a band (192)
 constexpr int CP_NBW = CP_COLS / 32 / 2;  // 32-column blocks per wave (3)
 static_assert(CP_COLS % 64 == 0, "a band is whole 32-column blocks for both column halves");
@@ -2150,7 +2153,7 @@ __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
     const bool BIAS1 = flags1 & CAMEL_EPI_BIAS, RELU1 = flags1 & CAMEL_EPI_RELU;
     const bool BIAS2 = flags2 & CAMEL_EPI_BIAS, RELU2 = flags2 & CAMEL_EPI_RELU;
     __shared__ __attribute__((aligned(16))) float patch[CP_C1 / 4 * CP_QPLANE];
-    __shared__ float img[CP_IR * CP_W];
+    __shared__ __attribute__((aligned(16))) float img[CP_IR * CP_W];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int half = lane >> 5, r32 = lane & 31;
     const int wm = wave & 1, wn = wave >> 1;
@@ -2170,40 +2173,36 @@ __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
         for (int s8 = 0; s8 < CP_C1 / 8; ++s8)
             a[j][s8] = *reinterpret_cast<const float4 *>(wr + j * CP_C1 + 8 * s8);
 
-    // The input rows of the band (zeros past the image: never read by a
-    // valid output, since the bands tile the pooled rows exactly).
-    const float *xi = x + (size_t)n * H * CP_W;
-    for (int i = tid; i < CP_IR * CP_W; i += 256) {
-        const int r = Y0 + i / CP_W;
-        img[i] = r < H ? xi[(size_t)Y0 * CP_W + i] : 0.f;
+    // conv1's weights and bias for this lane's channel (lane r32 computes
+    // channel r32 of one pixel; the two half-waves take two pixels).
+    float w1r[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) w1r[k] = w1[r32 * 9 + k];
+    const float b1r = BIAS1 ? b1[r32] : 0.f;
+
+    // The input rows of the band, 16 bytes per thread (zeros past the image:
+    // never read by a valid output, since the bands tile the pooled rows).
+    {
+        const float4 *xi = reinterpret_cast<const float4 *>(x + ((size_t)n * H + Y0) * CP_W);
+        if (tid < CP_IR * CP_W / 4) {
+            const int r = Y0 + tid / (CP_W / 4);
+            reinterpret_cast<float4 *>(img)[tid] = r < H ? xi[tid] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
     __syncthreads();
 
-    // conv1 into the patch: one pixel per thread, all channels; weights and
-    // bias are wave-uniform (scalar loads).
-    for (int p = tid; p < CP_R1 * CP_OW1; p += 256) {
+    // conv1 into the patch: the direct kernel's FMA chain, then bias and relu.
+    for (int p = 2 * wave + half; p < CP_R1 * CP_OW1; p += 8) {
         const int r = p / CP_OW1, c = p - r * CP_OW1;
-        float xv[9];
+        float acc = 0.f;
 #pragma unroll
         for (int kh = 0; kh < 3; ++kh)
 #pragma unroll
-            for (int kw = 0; kw < 3; ++kw) xv[kh * 3 + kw] = img[(r + kh) * CP_W + c + kw];
-        float *dst = patch + (r * CP_RS + c) * 4;
-#pragma unroll 2
-        for (int cq = 0; cq < CP_C1 / 4; ++cq) {
-            float4 q;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int ch = 4 * cq + u;
-                float acc = 0.f;
-#pragma unroll
-                for (int k = 0; k < 9; ++k) acc = __builtin_fmaf(w1[ch * 9 + k], xv[k], acc);
-                if (BIAS1) acc = acc + b1[ch];
-                if (RELU1) acc = relu_idiom(acc);
-                q[u] = acc;
-            }
-            *reinterpret_cast<float4 *>(dst + cq * CP_QPLANE) = q;
-        }
+            for (int kw = 0; kw < 3; ++kw)
+                acc = __builtin_fmaf(w1r[kh * 3 + kw], img[(r + kh) * CP_W + c + kw], acc);
+        if (BIAS1) acc = acc + b1r;
+        if (RELU1) acc = relu_idiom(acc);
+        patch[(r32 >> 2) * CP_QPLANE + (r * CP_RS + c) * 4 + (r32 & 3)] = acc;
     }
     __syncthreads();
 
@@ -2962,7 +2961,8 @@ int camel_hip_conv2d_pair_pool2(const float *x, const float *w1, const float *b1
         return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": null bias");
     if (N == 0) return ok();
     if (!x || !w1 || !w2 || !y) return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": null operand");
-    if (((uintptr_t)w2 & 15) != 0) return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": w2 not 16-byte aligned");
+    if ((((uintptr_t)w2 | (uintptr_t)x) & 15) != 0)
+        return fail(CAMEL_HIP_ERR_ARG, std::string(who) + ": x and w2 must be 16-byte aligned");
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
     const float *w2p = w2;
