@@ -60,7 +60,7 @@ def _traffic_entry(key: str):
                 for fld in fields[4:]:
                     if "=" in fld:
                         k, v = fld.split("=", 1)
-                        src[k] = v.split(",") if k == "kernels" else v
+                        src[k] = v.split(";") if k == "kernels" else v
                 return float(fields[0]), src
     except OSError:
         pass
