@@ -250,3 +250,26 @@ def test_division_by_zero_releases_the_abandoned_output():
         with pytest.raises(T.CamelError, match="Division by zero"):
             T.call("divide", a, z)
     assert T.live_count() == before
+
+
+def test_empty_operands_follow_the_reference():
+    # Zero-size operands through the operators (runtime.cpp's loops simply
+    # do not run): empty results keep their shapes, a K = 0 matmul is the
+    # zero-initialised output (operators.cpp:757-766 never adds a term), and
+    # the sum of nothing is 0.
+    e03, e34 = np.zeros((0, 3), F), D.uniform(0x7E00, (3, 4), -1.0, 1.0)
+    got = T.call("matmul", t(e03), t(e34)).numpy()
+    assert got.shape == (0, 4)
+    k0 = T.call("matmul", t(np.zeros((2, 0), F)), t(np.zeros((0, 4), F))).numpy()
+    np.testing.assert_array_equal(k0, O.matmul(np.zeros((2, 0), F), np.zeros((0, 4), F)))
+    assert not np.signbit(k0).any()
+    e05 = np.zeros((0, 5), F)
+    assert T.call("add", t(e05), t(e05)).numpy().shape == (0, 5)
+    assert T.call("multiply", t(e05), 2.0).numpy().shape == (0, 5)
+    assert T.call("relu", t(e05)).numpy().shape == (0, 5)
+    assert T.call("exp", t(e05)).numpy().shape == (0, 5)
+    assert T.call("softmax", t(np.zeros((0, 10), F))).numpy().shape == (0, 10)
+    assert T.call("transpose", t(e05)).numpy().shape == (5, 0)
+    assert T.call("sum", t(e05)) == O.sum_all(e05) == 0.0
+    w, b = D.uniform(0x7E01, (5, 7), -1.0, 1.0), np.zeros(7, F)
+    assert T.call("dense_relu", t(e05), with_=(t(w), t(b))).numpy().shape == (0, 7)
