@@ -1195,15 +1195,19 @@ int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, c
 //     needed; the accumulator of MFMA c holds rows 4 (l / 16) + v at column
 //     n0 + 4 (l % 16) + c.  Lane l's 8 k of a chunk are contiguous, so its A
 //     values are two 16-byte loads (A is small and stays in L2);
-//   * chunk c + 1 is in flight while chunk c is multiplied (register double
-//     buffer; scheduling barriers keep the compiler from sinking the loads
-//     next to their use);
-//   * the 8 waves' sums meet in LDS in wave order; work-groups along K
-//     (blockIdx.y) write partials [ks][M][N] that skinny_reduce_kernel sums
-//     in ks order before the epilogue (letting the last work-group of a
-//     strip do it needs device-scope release/acquire fences, and on this
-//     chip each one writes back or invalidates an XCD's whole L2: measured
-//     several times slower).
+//   * B is read with nontemporal loads (it is read once; they measured 7%
+//     faster than cached ones), a chunk's 8 loads issued together and
+//     multiplied once they land -- a register double buffer that kept the
+//     next chunk in flight measured 2% slower (the 8 waves of a CU already
+//     overlap one another's loads); scheduling barriers keep the compiler
+//     from interleaving a chunk's loads with its MFMAs;
+//   * the 8 waves' sums meet in LDS in wave order; thread x then owns row
+//     x / 16 and 4 consecutive columns, so the results (or the partials of
+//     work-groups along K, [ks][M][N], which skinny_reduce_kernel sums in ks
+//     order before the epilogue) leave as one 16-byte store per thread.
+//     Letting the last work-group of a strip add the partials needs
+//     device-scope release/acquire fences, and on this chip each one writes
+//     back or invalidates an XCD's whole L2: measured several times slower.
 // Work-groups whose rows, columns or k run past the operands take the same
 // loop with guarded scalar loads (a guarded load compiles to a branch, after
 // which the compiler waits for all loads at once, so full work-groups keep
@@ -1237,9 +1241,9 @@ __global__ __launch_bounds__(SK_WAVES * 64) void sgemm_skinny_kernel(
 
     auto stream_k = [&](auto full_tag) {
         constexpr bool FULL = decltype(full_tag)::value;
-        float4 b[2][S];
-        float4 a[2][MT][S / 4];
-        auto load = [&](int buf, int c) {
+        floatx4 b[S];
+        float4 a[MT][S / 4];
+        auto load = [&](int c) {
             const int kc = krow0 + c * SK_CHUNK;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
@@ -1248,48 +1252,43 @@ __global__ __launch_bounds__(SK_WAVES * 64) void sgemm_skinny_kernel(
                 for (int j = 0; j < S / 4; ++j) {
                     const int k = kc + 4 * j;
                     if (FULL) {
-                        a[buf][t][j] = *reinterpret_cast<const float4 *>(A + (size_t)row * K + k);
+                        a[t][j] = *reinterpret_cast<const float4 *>(A + (size_t)row * K + k);
                     } else {
                         float e[4];
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
                             e[i] = (row < M && k + i < K) ? A[(size_t)row * K + k + i] : 0.f;
-                        a[buf][t][j] = make_float4(e[0], e[1], e[2], e[3]);
+                        a[t][j] = make_float4(e[0], e[1], e[2], e[3]);
                     }
                 }
             }
 #pragma unroll
             for (int s = 0; s < S; ++s) {
                 const int k = kc + s;
-                b[buf][s] = (FULL || (col < N && k < K))
-                                ? *reinterpret_cast<const float4 *>(B + (size_t)k * N + col)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                b[s] = (FULL || (col < N && k < K))
+                           ? __builtin_nontemporal_load(
+                                 reinterpret_cast<const floatx4 *>(B + (size_t)k * N + col))
+                           : floatx4{0.f, 0.f, 0.f, 0.f};
             }
         };
-        auto multiply = [&](int buf) {
+        auto multiply = [&]() {
 #pragma unroll
             for (int s = 0; s < S; ++s)
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
-                    const float4 a4 = a[buf][t][s / 4];
+                    const float4 a4 = a[t][s / 4];
                     const float av = (s % 4 == 0) ? a4.x : (s % 4 == 1) ? a4.y : (s % 4 == 2) ? a4.z : a4.w;
-                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].x, acc[t][0], 0, 0, 0);
-                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].y, acc[t][1], 0, 0, 0);
-                    acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].z, acc[t][2], 0, 0, 0);
-                    acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[buf][s].w, acc[t][3], 0, 0, 0);
+                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[s][0], acc[t][0], 0, 0, 0);
+                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[s][1], acc[t][1], 0, 0, 0);
+                    acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[s][2], acc[t][2], 0, 0, 0);
+                    acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[s][3], acc[t][3], 0, 0, 0);
                 }
         };
-        load(0, 0);
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int c = 0; c < CH; c += 2) {
-            if (c + 1 < CH) load(1, c + 1);
+        for (int c = 0; c < CH; ++c) {
+            load(c);
             __builtin_amdgcn_sched_barrier(0);
-            multiply(0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (c + 2 < CH) load(0, c + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            if (c + 1 < CH) multiply(1);
+            multiply();
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -1306,67 +1305,68 @@ __global__ __launch_bounds__(SK_WAVES * 64) void sgemm_skinny_kernel(
                                                      acc[t][c][3]);
     __syncthreads();
 
-    // Thread x < MT*4*64 owns accumulator slot (t, c) of lane x % 64: rows
-    // 16 t + 4 (l / 16) + v, column n0 + 4 (l % 16) + c.
+    // Thread x < MT*256 owns row x / 16 and columns n0 + 4 (x % 16) .. +3.
+    // Row r = 16 t + 4 g + v sits in element v of accumulator (t, c) of lane
+    // 16 g + x % 16, for column n0 + 4 (x % 16) + c.
     const int x = threadIdx.x;
-    if (x >= MT * 4 * 64) return;
-    const int slot = x >> 6, sl = x & 63;
-    const int t = slot >> 2, c = slot & 3;
-    const int row0 = 16 * t + 4 * (sl >> 4), ocol = n0 + 4 * (sl & 15) + c;
-    if (ocol >= N) return;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (x >= MT * 256) return;
+    const int row = x >> 4, cg = x & 15;
+    const int ocol = n0 + 4 * cg;
+    if (row >= M || ocol >= N) return; // N % 4 == 0: a column group is all in or all out
+    const int t = row >> 4, sl = ((row & 15) >> 2) * 16 + cg, e = row & 3;
+    float v[4];
 #pragma unroll
-    for (int w = 0; w < SK_WAVES; ++w) {
-        const float4 p = red[w][slot][sl];
-        v[0] += p.x;
-        v[1] += p.y;
-        v[2] += p.z;
-        v[3] += p.w;
+    for (int c = 0; c < 4; ++c) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < SK_WAVES; ++w) s += reinterpret_cast<const float *>(&red[w][t * 4 + c][sl])[e];
+        v[c] = s;
     }
     if (nks == 1) {
-        const float bcol = (flags & CAMEL_EPI_BIAS) ? bias[ocol] : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = row0 + i;
-            if (row >= M) continue;
-            float y = v[i];
-            if (flags & CAMEL_EPI_BIAS) y = y + bcol;
+        for (int c = 0; c < 4; ++c) {
+            float y = v[c];
+            if (flags & CAMEL_EPI_BIAS) y = y + bias[ocol + c];
             if (flags & CAMEL_EPI_RELU) y = relu_idiom(y);
-            C[(size_t)row * N + ocol] = y;
+            v[c] = y;
         }
+        *reinterpret_cast<float4 *>(C + (size_t)row * N + ocol) = make_float4(v[0], v[1], v[2], v[3]);
         return;
     }
     // partial layout [ks][M][N]
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = row0 + i;
-        if (row < M) partial[((size_t)ks * M + row) * N + ocol] = v[i];
-    }
+    *reinterpret_cast<float4 *>(partial + ((size_t)ks * M + row) * N + ocol) =
+        make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // Sums the skinny kernel's k partials in ks order, then bias and relu; one
-// thread per 4 consecutive outputs of a row (N % 4 == 0).
-__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float4 *__restrict__ partial,
-                                                            float4 *__restrict__ C, int M, int N,
-                                                            int nks, const float *__restrict__ bias,
-                                                            int flags) {
+// thread per 4 consecutive outputs of a row (N % 4 == 0).  Small work-groups
+// (SK_REDUCE_THREADS) spread the few outputs over many CUs; the partials are
+// read once, with nontemporal loads.
+constexpr int SK_REDUCE_THREADS = 64;
+
+__global__ __launch_bounds__(SK_REDUCE_THREADS) void skinny_reduce_kernel(
+    const float4 *__restrict__ partial, float4 *__restrict__ C, int M, int N, int nks,
+    const float *__restrict__ bias, int flags) {
+    typedef float floatx4 __attribute__((ext_vector_type(4)));
     const size_t total4 = (size_t)M * N / 4;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= total4) return;
+    const floatx4 *p4 = reinterpret_cast<const floatx4 *>(partial);
     // k groups added in order; their loads go out up to 8 at a time
-    float4 y = partial[idx];
+    const floatx4 y0 = __builtin_nontemporal_load(p4 + idx);
+    float4 y = make_float4(y0[0], y0[1], y0[2], y0[3]);
     for (int z0 = 1; z0 < nks; z0 += 8) {
-        float4 p[8];
+        floatx4 p[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-            if (z0 + u < nks) p[u] = partial[(size_t)(z0 + u) * total4 + idx];
+            if (z0 + u < nks) p[u] = __builtin_nontemporal_load(p4 + (size_t)(z0 + u) * total4 + idx);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             if (z0 + u < nks) {
-                y.x = y.x + p[u].x;
-                y.y = y.y + p[u].y;
-                y.z = y.z + p[u].z;
-                y.w = y.w + p[u].w;
+                y.x = y.x + p[u][0];
+                y.y = y.y + p[u][1];
+                y.z = y.z + p[u][2];
+                y.w = y.w + p[u][3];
             }
         }
     }
@@ -1827,8 +1827,9 @@ int launch_skinny(const float *A, const float *B, float *C, int M, int N, int K,
         CAMEL_RETURN_IF(check_launch("sgemm_skinny_kernel"));
         if (nks == 1) return CAMEL_HIP_OK;
         const int64_t total4 = (int64_t)M * N / 4;
-        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((total4 + 255) / 256)), dim3(256),
-                           0, stream(), reinterpret_cast<const float4 *>(partial),
+        hipLaunchKernelGGL(skinny_reduce_kernel,
+                           dim3((unsigned)((total4 + SK_REDUCE_THREADS - 1) / SK_REDUCE_THREADS)),
+                           dim3(SK_REDUCE_THREADS), 0, stream(), reinterpret_cast<const float4 *>(partial),
                            reinterpret_cast<float4 *>(C), M, N, nks, bias, flags);
         return check_launch("skinny_reduce_kernel");
     };
