@@ -20,7 +20,7 @@ reference's CPU kernels, single thread) on a bounded row slab of the same
 workload, on this host, in this run.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-suite]
-       [--no-cpu] [--workload NAME]
+       [--no-cpu] [--workload NAME] [--vendor]
 """
 from __future__ import annotations
 
@@ -448,6 +448,105 @@ def cpu_baseline_bandwidth(kind: str, n: int = 1 << 24):
                      f"first {n} of 2^28 elements (slab) of {kind}", spent)
 
 
+# ------------------------------------------------------------ vendor line
+
+def vendor_suite() -> dict:
+    """The same workloads through PyTorch-ROCm's vendor libraries on this GPU
+    (hipBLASLt / rocBLAS GEMMs, MIOpen convolutions, torch's elementwise and
+    softmax kernels), fp32 with TF32-style shortcuts off, timed with events on
+    torch's current stream after >= 50 ms of warm-up.  A reference point for
+    the kernels of this library, not part of its product path."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    dev = torch.device("cuda", 0)
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+    def time_us(fn, iters):
+        t0 = time.perf_counter()
+        n = 0
+        while n < 5 or time.perf_counter() - t0 < SUITE_MIN_WARM_S:
+            fn()
+            n += 1
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / iters * 1e3
+
+    out = {}
+    for n in (256, 1024, 2048, 4096, 8192):
+        a = dt(D.uniform(D.SEED_GEMM + n, (n, n), -1.0, 1.0))
+        b = dt(D.uniform(D.SEED_GEMM + n + 1, (n, n), -1.0, 1.0))
+        c = torch.empty(n, n, device=dev)
+        us = time_us(lambda: torch.matmul(a, b, out=c), 10 if n >= 4096 else 200)
+        key = "matmul_256" if n == 256 else f"sgemm_{n}"
+        out[key] = {"us": round(us, 2), "TFLOP/s": round(2.0 * n ** 3 / us / 1e6, 2)}
+        del a, b, c
+    a = dt(D.uniform(D.SEED_GEMM + 16, (16, 4096), -1.0, 1.0))
+    bs = [dt(D.uniform(D.SEED_GEMM + 17 + 10 * s, (4096, 4096), -1.0, 1.0)) for s in range(6)]
+    c = torch.empty(16, 4096, device=dev)
+    it = [0]
+
+    def skinny():
+        torch.matmul(a, bs[it[0] % 6], out=c)
+        it[0] += 1
+    us = time_us(skinny, 600)
+    out["sgemm_16x4096x4096"] = {"us": round(us, 2),
+                                 "TB/s": round(4.0 * (2 * 16 * 4096 + 4096 * 4096) / us / 1e6, 3)}
+    del a, bs, c
+    dims = [784, 1024, 1024, 10]
+    x = dt(D.uniform(D.SEED_MLP, (1024, 784), 0.0, 1.0))
+    ws = [dt(D.normal(D.SEED_MLP + 1 + i, (dims[i], dims[i + 1]), std=float(np.sqrt(1.0 / dims[i]))))
+          for i in range(3)]
+    bz = [torch.zeros(d, device=dev) for d in dims[1:]]
+
+    def mlp():
+        h = torch.relu(torch.addmm(bz[0], x, ws[0]))
+        h = torch.relu(torch.addmm(bz[1], h, ws[1]))
+        return torch.softmax(torch.addmm(bz[2], h, ws[2]), dim=1)
+    us = time_us(mlp, 300)
+    out["mlp_forward"] = {"us": round(us, 2), "TFLOP/s": round(3.813e9 / us / 1e6, 2)}
+    xc = dt(D.normal(D.SEED_CONV_X, (64, 64, 56, 56)))
+    wc = dt(D.normal(D.SEED_CONV_W, (128, 64, 3, 3), std=float(np.sqrt(2.0 / 576))))
+    bc = torch.zeros(128, device=dev)
+    us = time_us(lambda: torch.relu(torch.nn.functional.conv2d(xc, wc, bc, padding=1)), 30)
+    out["conv2d_3x3"] = {"us": round(us, 2), "TFLOP/s": round(29.596e9 / us / 1e6, 2)}
+    del xc, wc
+    xi = dt(D.uniform(D.SEED_CNN, (512, 1, 28, 28), 0.0, 1.0))
+    w1 = dt(D.normal(D.SEED_CNN + 1, (32, 1, 3, 3), std=float(np.sqrt(2.0 / 9))))
+    w2 = dt(D.normal(D.SEED_CNN + 2, (64, 32, 3, 3), std=float(np.sqrt(2.0 / 288))))
+    w3 = dt(D.normal(D.SEED_CNN + 3, (9216, 128), std=float(np.sqrt(2.0 / 9216))))
+    w4 = dt(D.normal(D.SEED_CNN + 4, (128, 10), std=float(np.sqrt(2.0 / 128))))
+    z = {k: torch.zeros(k, device=dev) for k in (32, 64, 128, 10)}
+
+    def cnn():
+        h = torch.relu(torch.nn.functional.conv2d(xi, w1, z[32]))
+        h = torch.relu(torch.nn.functional.conv2d(h, w2, z[64]))
+        h = torch.nn.functional.max_pool2d(h, 2).reshape(512, 9216)
+        h = torch.relu(torch.addmm(z[128], h, w3))
+        return torch.softmax(torch.addmm(z[10], h, w4), dim=1)
+    us = time_us(cnn, 50)
+    out["cnn_forward"] = {"us": round(us, 2), "TFLOP/s": round(12.28e9 / us / 1e6, 2)}
+    n = 1 << 28
+    ea = torch.rand(n, device=dev) * 2 - 1
+    eb = torch.rand(n, device=dev) * 2 - 1
+    ec = torch.empty(n, device=dev)
+    for name, fn, nb in (("eltwise_add", lambda: torch.add(ea, eb, out=ec), 12.0),
+                         ("eltwise_mul", lambda: torch.mul(ea, eb, out=ec), 12.0),
+                         ("eltwise_relu", lambda: torch.clamp_min(ea, 0.0, out=ec), 8.0)):
+        us = time_us(fn, 20)
+        out[name] = {"us": round(us, 2), "TB/s": round(nb * n / us / 1e6, 3)}
+    del ea, eb, ec
+    sx = torch.randn(262144, 1024, device=dev)
+    us = time_us(lambda: torch.softmax(sx, dim=1), 20)
+    out["softmax_262144x1024"] = {"us": round(us, 2), "TB/s": round(8.0 * 262144 * 1024 / us / 1e6, 3)}
+    return {"vendor": out, "torch": torch.__version__}
+
+
 # ------------------------------------------------------------------- main
 
 def main() -> int:
@@ -459,6 +558,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--unfused", action="store_true",
                     help="mlp / cnn workloads: one call per layer (no fused kernels)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="time the same workloads through PyTorch-ROCm's vendor libraries instead")
     ap.add_argument("--workload", default="gemm4096",
                     choices=["gemm4096", "mlp", "conv2d", "cnn", "eltwise", "softmax", "skinny",
                              "copy"])
@@ -468,6 +569,10 @@ def main() -> int:
         print("bench.py: this build runs on one GPU only; multi-GPU runs are not supported "
               "(use --gpus 1)", file=sys.stderr)
         return 2
+
+    if args.vendor:
+        print(json.dumps(vendor_suite()))
+        return 0
 
     H.call("camel_hip_init", 0)
     steps, warmup = args.steps, args.warmup
