@@ -245,18 +245,19 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         float4 rbn[is_nhwc<BMODE> ? T::BN_ITEMS : 1];
     };
     StageRegs R0;
-    // LOAD_VEC B on the long-stage (non-EARLY) tiles: each item's pointer to
-    // its first k row, advanced BK rows per loaded stage, in place of a
-    // 64-bit multiply per load and stage (measured 1% faster at 4096^3; the
-    // EARLY tiles keep the multiply, 7% faster there at 1024^3).
+    // LOAD_VEC B on the long-stage (non-EARLY) tiles: each item's element
+    // offset of its first k row, advanced BK rows per loaded stage, in place
+    // of a 64-bit multiply per load and stage (measured 1% faster at 4096^3;
+    // the EARLY tiles keep the multiply, 7% faster there at 1024^3).  An
+    // offset rather than a pointer: the ragged first stage starts below row 0.
     constexpr bool B_PTR = BMODE == LOAD_VEC && !T::EARLY;
-    const float *b_vec_ptr[B_PTR ? T::B_ITEMS : 1];
+    ptrdiff_t b_vec_off[B_PTR ? T::B_ITEMS : 1];
     if constexpr (B_PTR) {
 #pragma unroll
         for (int i = 0; i < T::B_ITEMS; ++i) {
             const int q = tid + i * T::THREADS;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
-            b_vec_ptr[i] = g.B + (ptrdiff_t)(kbeg + 4 * kq) * g.ldb + n0 + 4 * nq;
+            b_vec_off[i] = (ptrdiff_t)(kbeg + 4 * kq) * g.ldb + n0 + 4 * nq;
         }
     }
 
@@ -409,13 +410,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
-                    const float *src = B_PTR ? b_vec_ptr[i] + (ptrdiff_t)u * g.ldb
+                    const float *src = B_PTR ? g.B + (b_vec_off[i] + (ptrdiff_t)u * g.ldb)
                                              : g.B + (size_t)gk * g.ldb + gn;
                     rb[i][u] = (FULL || (gn < g.N && gk >= 0 && gk < kend))
                                    ? *reinterpret_cast<const float4 *>(src)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
-                if constexpr (B_PTR) b_vec_ptr[i] += (ptrdiff_t)T::BK * g.ldb;
+                if constexpr (B_PTR) b_vec_off[i] += (ptrdiff_t)T::BK * g.ldb;
             } else if constexpr (BMODE == LOAD_SCALAR) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
