@@ -178,6 +178,9 @@ def test_skinny_gemm_matches_oracle():
     (32, 4096, 4096),   # two 16-row groups, four chunks per work-group
     (16, 1024, 4099),   # K % 4 != 0: every work-group takes the guarded loads
     (8, 2048, 8192),    # M < 16: rows past M read as zero
+    (20, 64, 100),      # two 16-row groups, one work-group, no partials
+    (32, 128, 256),     # two full 16-row groups, one k group per strip
+    (17, 4096, 4096),   # one row past a 16-row group, four k groups per strip
 ])
 def test_skinny_streaming_kernel_matches_oracle(M, N, Kd):
     # M <= 32, N % 4 == 0: the streaming kernel (16x16x4 MFMA), k partials
