@@ -350,7 +350,8 @@ def test_cnn_chain_full_batch_is_exact(_release):
     full.release()
 
 
-@pytest.mark.parametrize("M,N,Kd", [(16, 4096, 4096), (32, 4096, 8192), (8, 1000, 20000)])
+@pytest.mark.parametrize("M,N,Kd", [(16, 4096, 4096), (32, 4096, 8192), (8, 1000, 20000),
+                                     (24, 64, 200)])
 def test_skinny_split_sums_are_exact_on_every_call(M, N, Kd):
     # The streaming kernel's k partials and their ordered reduce: 40 calls in
     # a row into an output pre-filled with NaN, each bit-exact (a partial read
