@@ -535,9 +535,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     //     stage kt+1 issued right after it, so those MFMAs cover the read
     //     latency and the barrier costs little more than the waves' skew
     //     (measured faster for 64x64 and 128x128 tiles);
-    //   * otherwise: all G groups, then the store and the barrier (measured
+    //   * otherwise: stage kt+1 is stored to the other buffer right after the
+    //     first group's MFMAs, and the barrier follows all G groups (measured
     //     faster for the 8-wave 256x256 tile, whose long stages already hide
-    //     the barrier).
+    //     the barrier; storing after the first group rather than after the
+    //     last keeps the stores' latency off the end of the stage: 4096^3
+    //     134.4-136.9 -> 137.3-138.0 TFLOP/s, and after the second or third
+    //     group was slower, 137.3 / 133.2).
     constexpr int GROUPS = T::BK / 8 / T::WK; // 8-k groups of this wave's k-group
     constexpr int STORE_AT = GROUPS / 2 - 1;   // store after this group's MFMAs
     static_assert(GROUPS % 2 == 0, "operand registers alternate between even and odd groups");
@@ -591,8 +595,9 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                     if (s8 + 1 < GROUPS) __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
                     mfma_group(fa[cur], fb[cur]);
                     __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
+                    if (s8 == 0 && more)
+                        store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
                 }
-                if (more) store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
                 __syncthreads();
             }
             return;
