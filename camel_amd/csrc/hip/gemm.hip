@@ -528,8 +528,9 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     //   * the global loads of stage kt+1 are issued first (registers);
     //   * LDS operand reads run one 8-k group ahead of the MFMAs that use them,
     //     so each group's ds_read latency hides behind the previous group's
-    //     MFMAs (on the 256x256 tile they are spread one per two MFMAs over
-    //     the head of the group, 1% faster at 4096^3 than issued together);
+    //     MFMAs; they are spread one per two MFMAs over the head of the group
+    //     (measured against issuing them together before it: 4096^3 1-2%,
+    //     2048^3 1.5%, the config-4 conv 3.7% faster);
     //   * EARLY: halfway through, stage kt+1 is stored to the other LDS buffer
     //     (its last readers finished before the previous barrier), and the
     //     barrier comes before the last group's MFMAs, with the first reads of
@@ -545,6 +546,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     //     group was slower, 137.3 / 133.2).
     constexpr int GROUPS = T::BK / 8 / T::WK; // 8-k groups of this wave's k-group
     constexpr int STORE_AT = GROUPS / 2 - 1;   // store after this group's MFMAs
+    // MFMAs between two of the next group's operand reads (the reads are
+    // spread over the head of a group; all tiles have 4 FM FN >= 2 (FM + FN)).
+    constexpr int READ_SPACING = 2;
+    static_assert(4 * T::FM * T::FN >= READ_SPACING * (T::FM + T::FN), "read spacing");
     static_assert(GROUPS % 2 == 0, "operand registers alternate between even and odd groups");
     auto operand_bases = [&](int kt, const float *&a_base, const float *&b_base) {
         const float *As = smem + (kt & 1) * T::STAGE;
@@ -592,17 +597,18 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int s8 = 0; s8 < GROUPS; ++s8) {
                     const int cur = s8 & 1;
-                    // the next group's operand reads go out one per two MFMAs
-                    // at the head of this group
+                    // the next group's operand reads go out one per
+                    // READ_SPACING MFMAs at the head of this group
                     if (s8 + 1 < GROUPS) fetch(a_base, b_base, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
                     mfma_group(fa[cur], fb[cur]);
                     if (s8 + 1 < GROUPS) {
 #pragma unroll
                         for (int r = 0; r < T::FM + T::FN; ++r) {
-                            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x008, READ_SPACING, 0);
                             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                         }
-                        __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN - 2 * (T::FM + T::FN), 0);
+                        __builtin_amdgcn_sched_group_barrier(
+                            0x008, 4 * T::FM * T::FN - READ_SPACING * (T::FM + T::FN), 0);
                     } else {
                         __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
                     }
@@ -622,11 +628,16 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             for (int s8 = 0; s8 + 1 < GROUPS; ++s8) {
                 const int cur = s8 & 1;
                 fetch(a_base, b_base, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
-                // Keep the order: the next group's LDS reads issue before this
-                // group's MFMAs (masks: 0x100 LDS read, 0x8 MFMA).
-                __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
                 mfma_group(fa[cur], fb[cur]);
-                __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
+                // The next group's LDS reads go out one per READ_SPACING MFMAs
+                // at the head of this group (masks: 0x100 LDS read, 0x8 MFMA).
+#pragma unroll
+                for (int r = 0; r < T::FM + T::FN; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, READ_SPACING, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(
+                    0x008, 4 * T::FM * T::FN - READ_SPACING * (T::FM + T::FN), 0);
                 if (s8 == STORE_AT && more)
                     store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
             }
