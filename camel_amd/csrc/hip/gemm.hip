@@ -2294,11 +2294,12 @@ __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
     for (int b = 0; b < CP_NBW; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
-    // Each (kh, kw) stage issues the weight loads of stage + 2 first; within
-    // a stage the patch reads of the next 8-channel group go out one per two
-    // of the current group's MFMAs (scheduling group barriers keep that
-    // order; 3.7% faster over the CNN forward than issuing them together
-    // ahead of the MFMAs).
+    // Each 8-channel group of a (kh, kw) stage loads the same group's weights
+    // of stage + 2 and reads the next group's patch values, spread over its
+    // own MFMAs: one patch read per two MFMAs, then the weight load
+    // (scheduling group barriers keep that order; 4% faster over the CNN
+    // forward than the reads together ahead of the MFMAs and the stage's
+    // weight loads together at its start).
     auto patch_reads = [&](int khw, int s8, float4 *bv) {
         const int kh = khw / 3, kw = khw - 3 * (khw / 3);
         const int off = 2 * s8 * CP_QPLANE + (kh * CP_RS + kw) * 4;
@@ -2311,17 +2312,15 @@ __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
 #pragma unroll
     for (int khw = 0; khw < 9; ++khw) {
         const int cur = khw % 3;
-        if (khw + 2 < 9) {
-#pragma unroll
-            for (int s8 = 0; s8 < CP_C1 / 8; ++s8)
-                a[(khw + 2) % 3][s8] =
-                    *reinterpret_cast<const float4 *>(wr + (khw + 2) * CP_C1 + 8 * s8);
-        }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s8 = 0; s8 < CP_C1 / 8; ++s8) {
             const int g = khw * (CP_C1 / 8) + s8; // group index over all of K
             const bool next = g + 1 < 9 * (CP_C1 / 8);
+            const bool ahead = khw + 2 < 9;
+            // group s8's weights of stage khw + 2
+            if (ahead)
+                a[(khw + 2) % 3][s8] =
+                    *reinterpret_cast<const float4 *>(wr + (khw + 2) * CP_C1 + 8 * s8);
             if (next) patch_reads((g + 1) / (CP_C1 / 8), (g + 1) % (CP_C1 / 8), bv[(g + 1) & 1]);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
@@ -2330,13 +2329,21 @@ __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
                     acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][s8][t], bv[g & 1][b][t],
                                                                   acc[b], 0, 0, 0);
             if (next) {
-                // one patch read per two MFMAs at the head of the group
+                // one patch read per two MFMAs at the head of the group, then
+                // the weight load after one more MFMA (masks: 0x100 LDS read,
+                // 0x20 global read, 0x8 MFMA)
 #pragma unroll
                 for (int r = 0; r < CP_NBW; ++r) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, 2 * CP_NBW, 0);
+                if (ahead) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * CP_NBW - 1, 0);
+                } else {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * CP_NBW, 0);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
