@@ -624,15 +624,18 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         // Plain GEMM tiles (A and B row-major, 16-byte loads): with 32x32
         // wave tiles the next stage's loads go out after the first group's
         // operand reads rather than ahead of them (0.6% at 1024^3, 0.4 us of
-        // the MLP's 47.7); where a group has MFMAs to spare, the next stage's
-        // LDS stores are spread one per MFMA over the group after STORE_AT
-        // rather than issued together after it (0.5% at 2048^3).
+        // the MLP's 47.7).  Plain and (pixel, k-quad) conv tiles with MFMAs to
+        // spare spread the next stage's LDS stores one per MFMA over the
+        // group after STORE_AT rather than issuing them together after it
+        // (0.5% at 2048^3 and at the config-4 conv).
         constexpr bool PLAIN = AMODE == LOAD_VEC && BMODE == LOAD_VEC;
+        constexpr bool PIXEL_B = AMODE == LOAD_VEC && is_nhwc<BMODE>;
         constexpr int NMF = 4 * T::FM * T::FN, NRD = T::FM + T::FN;
-        constexpr int NST = T::A_ITEMS + 4 * T::B_ITEMS; // LDS stores per stage (plain)
+        // LDS stores per stage
+        constexpr int NST = T::A_ITEMS + (PIXEL_B ? T::BN_ITEMS : 4 * T::B_ITEMS);
         constexpr bool LATE_LOADS = PLAIN && T::FM * T::FN == 1;
         constexpr bool SPREAD_STORES =
-            PLAIN && GROUPS >= 4 && NMF - READ_SPACING * NRD >= NST;
+            (PLAIN || PIXEL_B) && GROUPS >= 4 && NMF - READ_SPACING * NRD >= NST;
         for (int kt = 0; kt < nk; ++kt) {
             const bool more = kt + 1 < nk;
             if (!LATE_LOADS && more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0);
