@@ -71,6 +71,12 @@ template <int M> constexpr bool is_planes = (M == LOAD_PLANES || M == LOAD_PLANE
 template <int M> constexpr bool is_pool = (M == LOAD_NHWC_POOL || M == LOAD_PLANES_POOL);
 template <int M> constexpr bool is_conv = (M == LOAD_CONV || is_nhwc<M>);
 
+// Operands one call of a kernel's stage loader fetches.
+enum LoadPart { LOAD_BOTH = 0, LOAD_A_ONLY = 1, LOAD_B_ONLY = 2 };
+constexpr std::integral_constant<int, LOAD_BOTH> load_ab{};
+constexpr std::integral_constant<int, LOAD_A_ONLY> load_a{};
+constexpr std::integral_constant<int, LOAD_B_ONLY> load_b{};
+
 // WK > 1 splits each stage's K range over WK groups of WM x WN waves (more
 // waves per CU to hide latency when there are few tiles); the groups' sums
 // meet in LDS at the end, added in group order.  EARLY selects the stage
@@ -327,14 +333,18 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     // FULL: the tile lies inside M x N and the stage is a whole BK inside
     // [0, K), so the row/column/k guards compile away (every stage of the
     // interior tiles but a ragged first one).
-    auto load_stage = [&](auto full_tag, int k0, StageRegs &R) {
+    // part_tag (LoadPart) picks the operands: both, or A or B alone (a
+    // stage's loads split over two MFMA groups).
+    auto load_stage = [&](auto full_tag, int k0, StageRegs &R, auto part_tag) {
         constexpr bool FULL = decltype(full_tag)::value;
+        constexpr bool LA = decltype(part_tag)::value != LOAD_B_ONLY;
+        constexpr bool LB = decltype(part_tag)::value != LOAD_A_ONLY;
         float4 *ra = R.ra;
         auto &rat = R.rat;
         auto &rb = R.rb;
         float4 *rbn = R.rbn;
 #pragma unroll
-        for (int i = 0; i < (is_trans<AMODE> ? T::A_T_ITEMS : 0); ++i) {
+        for (int i = 0; i < (is_trans<AMODE> && LA ? T::A_T_ITEMS : 0); ++i) {
             // item (kq, mq): rows k0+4kq .. +3 of At, columns m0+4mq .. +3
             // (vector) or m0+mq+c*BM/4 (scalar, c = 0..3)
             const int q = tid + i * T::THREADS;
@@ -361,7 +371,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < (is_trans<AMODE> ? 0 : T::A_ITEMS); ++i) {
+        for (int i = 0; i < (is_trans<AMODE> || !LA ? 0 : T::A_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             if (A_TAIL && q >= T::A_TOTAL) break;
             const int kq = q % T::KQ, m = q / T::KQ;
@@ -379,7 +389,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 ra[i].w = (rv && (FULL || (gk + 3 >= 0 && gk + 3 < kend))) ? src[3] : 0.f;
             }
         }
-        if constexpr (is_nhwc<BMODE>) {
+        if constexpr (is_nhwc<BMODE> && LB) {
             // k0 .. k0+BK-1 share (kh, kw): channels c0 .. c0+BK-1.
             const int khw = k0 / g.Cin, c0 = k0 - khw * g.Cin;
             const int kh = khw / g.KW, kw = khw - kh * g.KW;
@@ -401,7 +411,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             }
         }
 #pragma unroll
-        for (int i = 0; i < (is_nhwc<BMODE> ? 0 : T::B_ITEMS); ++i) {
+        for (int i = 0; i < (is_nhwc<BMODE> || !LB ? 0 : T::B_ITEMS); ++i) {
             const int q = tid + i * T::THREADS;
             if (B_TAIL && q >= T::B_TOTAL) break;
             const int nq = q % (T::BN / 4), kq = q / (T::BN / 4);
@@ -543,7 +553,14 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     //     the barrier; storing after the first group rather than after the
     //     last keeps the stores' latency off the end of the stage: 4096^3
     //     134.4-136.9 -> 137.3-138.0 TFLOP/s, and after the second or third
-    //     group was slower, 137.3 / 133.2).
+    //     group was slower, 137.3 / 133.2).  With 16-byte A and B loads and
+    //     at least 3 groups, the global loads run two stages ahead: stage
+    //     kt+2's A rows go out among the MFMAs of group G-2 of stage kt and
+    //     its B rows among those of group G-1, into the registers the store
+    //     after group 0 has just emptied, instead of all at the top of
+    //     stage kt+1 (4096^3 139.6 -> 142.0 TFLOP/s, 8192^3 141.0 -> 143.3;
+    //     the loads in groups 1-2, or spaced 1 to 5 MFMAs apart, gained
+    //     only 139.4-139.7).
     constexpr int GROUPS = T::BK / 8 / T::WK; // 8-k groups of this wave's k-group
     constexpr int STORE_AT = GROUPS / 2 - 1;   // store after this group's MFMAs
     // MFMAs between two of the next group's operand reads (the reads are
@@ -580,37 +597,64 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     auto main_loop = [&](auto full_tag) {
         if (nk <= 0) return;
         if (kbeg < 0)
-            load_stage(std::false_type{}, kbeg, R0); // the ragged first stage
+            load_stage(std::false_type{}, kbeg, R0, load_ab); // the ragged first stage
         else
-            load_stage(full_tag, kbeg, R0);
+            load_stage(full_tag, kbeg, R0, load_ab);
         store_stage(smem, smem + T::A_STAGE, R0);
         __syncthreads();
         float4 fa[2][T::FM], fb[2][T::FN];
         const float *a_base, *b_base;
         if constexpr (!T::EARLY) {
+            // AHEAD: loads two stages ahead, split over the last two groups
+            constexpr bool AHEAD = AMODE == LOAD_VEC && BMODE == LOAD_VEC && GROUPS >= 3;
+            constexpr int NMF = 4 * T::FM * T::FN, NRD = T::FM + T::FN;
+            constexpr int NLA = T::A_ITEMS, NLB = 4 * T::B_ITEMS; // 16-byte loads
+            static_assert(!AHEAD || (NMF >= READ_SPACING * (NRD + NLA) && NMF >= READ_SPACING * NLB),
+                          "loads two stages ahead fit among a group's MFMAs");
+            if (AHEAD && nk > 1) load_stage(full_tag, kbeg + T::BK, R0, load_ab);
             for (int kt = 0; kt < nk; ++kt) {
-                const bool more = kt + 1 < nk;
-                if (more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0);
+                const bool more = kt + 1 < nk, more2 = kt + 2 < nk;
+                if (!AHEAD && more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0, load_ab);
                 operand_bases(kt, a_base, b_base);
                 fetch(a_base, b_base, 0, fa[0], fb[0]);
-                __builtin_amdgcn_sched_group_barrier(0x100, T::FM + T::FN, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
 #pragma unroll
                 for (int s8 = 0; s8 < GROUPS; ++s8) {
                     const int cur = s8 & 1;
                     // the next group's operand reads go out one per
                     // READ_SPACING MFMAs at the head of this group
                     if (s8 + 1 < GROUPS) fetch(a_base, b_base, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                    if (AHEAD && s8 == GROUPS - 2 && more2)
+                        load_stage(full_tag, kbeg + (kt + 2) * T::BK, R0, load_a);
+                    if (AHEAD && s8 == GROUPS - 1 && more2)
+                        load_stage(full_tag, kbeg + (kt + 2) * T::BK, R0, load_b);
                     mfma_group(fa[cur], fb[cur]);
                     if (s8 + 1 < GROUPS) {
 #pragma unroll
-                        for (int r = 0; r < T::FM + T::FN; ++r) {
+                        for (int r = 0; r < NRD; ++r) {
                             __builtin_amdgcn_sched_group_barrier(0x008, READ_SPACING, 0);
                             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                         }
-                        __builtin_amdgcn_sched_group_barrier(
-                            0x008, 4 * T::FM * T::FN - READ_SPACING * (T::FM + T::FN), 0);
+                        if (AHEAD && s8 == GROUPS - 2) {
+#pragma unroll
+                            for (int r = 0; r < NLA; ++r) {
+                                __builtin_amdgcn_sched_group_barrier(0x008, READ_SPACING, 0);
+                                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                            }
+                            __builtin_amdgcn_sched_group_barrier(
+                                0x008, NMF - READ_SPACING * (NRD + NLA), 0);
+                        } else {
+                            __builtin_amdgcn_sched_group_barrier(0x008, NMF - READ_SPACING * NRD, 0);
+                        }
+                    } else if (AHEAD) {
+#pragma unroll
+                        for (int r = 0; r < NLB; ++r) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, READ_SPACING, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x008, NMF - READ_SPACING * NLB, 0);
                     } else {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);
                     }
                     if (s8 == 0 && more)
                         store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
@@ -638,13 +682,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             (PLAIN || PIXEL_B) && GROUPS >= 4 && NMF - READ_SPACING * NRD >= NST;
         for (int kt = 0; kt < nk; ++kt) {
             const bool more = kt + 1 < nk;
-            if (!LATE_LOADS && more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0);
+            if (!LATE_LOADS && more) load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0, load_ab);
 #pragma unroll
             for (int s8 = 0; s8 + 1 < GROUPS; ++s8) {
                 const int cur = s8 & 1;
                 fetch(a_base, b_base, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
                 if (LATE_LOADS && s8 == 0 && more)
-                    load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0);
+                    load_stage(full_tag, kbeg + (kt + 1) * T::BK, R0, load_ab);
                 const bool spread = SPREAD_STORES && s8 == STORE_AT + 1;
                 if (spread && more)
                     store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
