@@ -115,7 +115,9 @@ GEMM_SHAPES = [
     (256, 256, 256, 0, "config 1: 32x32 tiles, four k-groups, K splits"),
     (1024, 1024, 1024, 3, "64x64 tiles with two k-groups, one tile per CU"),
     (1024, 1024, 784, 3, "MLP layer 1: 64x64 tiles, ragged first K stage"),
-    (2048, 2048, 2048, 0, "128x128 tiles, one round"),
+    (2048, 2048, 2048, 0, "128x128 tiles, one round: 8 waves in two k-groups"),
+    (2000, 2100, 1000, 3, "128x128 two-k-group tiles, ragged edges, K % 64 = 40"),
+    (2048, 4096, 2048, 0, "128x128 tiles, two rounds: 4 waves"),
     (4096, 4096, 4096, 0, "headline: 8-wave 256x256 tiles, one round, XCD remap"),
     (8192, 8192, 8192, 0, "256x256 tiles, four rounds"),
     (4352, 4352, 512, 3, "256x256 whole round + K-split tail + ordered reduce"),

@@ -45,6 +45,7 @@ def test_sgemm_matches_oracle(M, N, Kd):
     (512, 256, 2000),    # 64x64 tiles, 7 K splits, K % 64 = 16
     (1024, 2048, 1000),  # 64x64 tiles, no split, K % 64 = 40
     (2048, 2048, 1001),  # 128x128 tiles, odd K (scalar A loads), K % 32 = 9
+    (2000, 2100, 1000),  # 128x128 tiles in two k-groups (one round), K % 64 = 40
     (4096, 4096, 1000),  # 256x256 tiles, K % 32 = 8
     (200, 72, 1000),     # 32x32 tiles, K splits, K % 64 = 40
 ])
