@@ -334,8 +334,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     // [0, K), so the row/column/k guards compile away (every stage of the
     // interior tiles but a ragged first one).
     // part_tag (LoadPart) picks the operands: both, or A or B alone (a
-    // stage's loads split over two MFMA groups).
-    auto load_stage = [&](auto full_tag, int k0, StageRegs &R, auto part_tag) {
+    // stage's loads split over two MFMA groups).  again: k0 is the stage
+    // loaded last, read once more (the B row offsets step back a stage and
+    // are not advanced).
+    auto load_stage = [&](auto full_tag, int k0, StageRegs &R, auto part_tag, bool again = false) {
         constexpr bool FULL = decltype(full_tag)::value;
         constexpr bool LA = decltype(part_tag)::value != LOAD_B_ONLY;
         constexpr bool LB = decltype(part_tag)::value != LOAD_A_ONLY;
@@ -420,13 +422,14 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
-                    const float *src = B_PTR ? g.B + (b_vec_off[i] + (ptrdiff_t)u * g.ldb)
+                    const ptrdiff_t back = again ? (ptrdiff_t)T::BK * g.ldb : 0;
+                    const float *src = B_PTR ? g.B + (b_vec_off[i] - back + (ptrdiff_t)u * g.ldb)
                                              : g.B + (size_t)gk * g.ldb + gn;
                     rb[i][u] = (FULL || (gn < g.N && gk >= 0 && gk < kend))
                                    ? *reinterpret_cast<const float4 *>(src)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
-                if constexpr (B_PTR) b_vec_off[i] += (ptrdiff_t)T::BK * g.ldb;
+                if constexpr (B_PTR) b_vec_off[i] += again ? 0 : (ptrdiff_t)T::BK * g.ldb;
             } else if constexpr (BMODE == LOAD_SCALAR) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
@@ -624,10 +627,11 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                     // the next group's operand reads go out one per
                     // READ_SPACING MFMAs at the head of this group
                     if (s8 + 1 < GROUPS) fetch(a_base, b_base, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
-                    if (AHEAD && s8 == GROUPS - 2 && more2)
-                        load_stage(full_tag, kbeg + (kt + 2) * T::BK, R0, load_a);
-                    if (AHEAD && s8 == GROUPS - 1 && more2)
-                        load_stage(full_tag, kbeg + (kt + 2) * T::BK, R0, load_b);
+                    // Past the end the last stage is read again (in bounds,
+                    // never stored): no branch splits the loop body.
+                    const int k2 = kbeg + (more2 ? kt + 2 : nk - 1) * T::BK;
+                    if (AHEAD && s8 == GROUPS - 2) load_stage(full_tag, k2, R0, load_a, !more2);
+                    if (AHEAD && s8 == GROUPS - 1) load_stage(full_tag, k2, R0, load_b, !more2);
                     mfma_group(fa[cur], fb[cur]);
                     if (s8 + 1 < GROUPS) {
 #pragma unroll
@@ -656,7 +660,11 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                     } else {
                         __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);
                     }
-                    if (s8 == 0 && more)
+                    // Unconditional: after the last stage this stores stale
+                    // registers to the buffer the previous stage read, which
+                    // no wave reads again (4096^3 +0.6%, 8192^3 +1.2% over
+                    // a branch on kt + 1 < nk).
+                    if (s8 == 0)
                         store_stage(lds_stage(kt + 1), lds_stage(kt + 1) + T::A_STAGE, R0);
                 }
                 __syncthreads();
