@@ -732,7 +732,11 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
         }
     };
-    const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N);
+    // The branch-free loop reads its last stage again past the end, unguarded
+    // in a full tile, so that stage must be whole: a split whose only stage
+    // is the ragged first one (K < BK) runs the guarded loop.
+    const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N) &&
+                           !(nk == 1 && kbeg < 0);
     if (full_tile)
         main_loop(std::true_type{});
     else

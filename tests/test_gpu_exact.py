@@ -118,6 +118,10 @@ GEMM_SHAPES = [
     (2048, 2048, 2048, 0, "128x128 tiles, one round: 8 waves in two k-groups"),
     (2000, 2100, 1000, 3, "128x128 two-k-group tiles, ragged edges, K % 64 = 40"),
     (2048, 4096, 2048, 0, "128x128 tiles, two rounds: 4 waves"),
+    (4096, 4096, 20, 3, "256x256 tiles, K < BK: one ragged stage, guarded loop"),
+    (4096, 4096, 40, 0, "256x256 tiles, a ragged stage then a whole one read again"),
+    (2048, 2048, 40, 3, "two-k-group 128x128 tiles, K < BK: one ragged stage"),
+    (2048, 2048, 100, 0, "two-k-group 128x128 tiles, ragged stage + one whole stage"),
     (4096, 4096, 4096, 0, "headline: 8-wave 256x256 tiles, one round, XCD remap"),
     (8192, 8192, 8192, 0, "256x256 tiles, four rounds"),
     (4352, 4352, 512, 3, "256x256 whole round + K-split tail + ordered reduce"),
