@@ -272,8 +272,9 @@ int ot_argmax_axis(int dt, const void *x, int64_t rows, int64_t cols, int64_t ax
     return OT_OK;
 }
 
-/* tensorExp, runtime.cpp:1013-1026.  Parity unpinned at the libm boundary:
- * glibc exp() is the third-party routine; checked against closed forms only. */
+/* tensorExp, runtime.cpp:1013-1026.  glibc exp() is the third-party routine
+ * at the libm boundary; the tests pin it element for element against Python's
+ * math.exp (the same glibc) and against closed forms. */
 int ot_exp(int dt, const void *x, float *out, uint64_t n) {
     if (dt != OT_F32) return OT_ERR_DTYPE;
     for (uint64_t i = 0; i < n; ++i) out[i] = (float)exp(ot_get(dt, x, i));
@@ -379,9 +380,9 @@ int ot_dense(const float *x, const float *W, const float *b, int relu, float *ou
 /* conv2d NCHW, no reference op: defined as im2col(x) @ W^T with the matmul
  * semantics of operators.cpp:757-766 -- one double accumulator per output,
  * k = (c, kh, kw) ascending, zero padding contributes its 0.0 * w terms --
- * then the bias add and relu idioms as in ot_dense.  Parity unpinned by the
- * reference (no op); pinned by equivalence with ot_matmul on an explicit
- * im2col and by brute force on tiny shapes. */
+ * then the bias add and relu idioms as in ot_dense.  The reference has no
+ * conv op to compare with; the tests pin this one by equivalence with
+ * ot_matmul on an explicit im2col and by integer brute force on tiny shapes. */
 int64_t ot_conv2d_images(const float *x, const float *w, const float *b, int relu, float *y,
                          int64_t n_begin, int64_t n_end, int64_t C, int64_t H, int64_t W,
                          int64_t Co, int64_t KH, int64_t KW, int64_t stride, int64_t pad) {
