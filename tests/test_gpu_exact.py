@@ -18,6 +18,18 @@ could not see it.
 
 Every kernel path of the GEMM and conv entry points is reached at its
 benchmark shape (the path each shape takes is named beside it).
+
+Operands in [-2, 2] are exact in bf16 as well, so they cannot tell an fp32
+MFMA from one fed narrower operands.  The wide-operand tests therefore give
+one operand integers with |x| <= 4095 (12 significant bits: exact in fp32,
+rounded in bf16's 8 and in fp16's or tf32's 11) and the other {-1, 0, 1}
+with at most 4000 nonzeros per dot product, so sum |a||b| + |bias| < 2**24
+still holds for every output: every product is a wide value or 0, every
+partial sum an exact integer, and rounding either operand to a narrower
+type moves outputs (tests/test_exact_operands.py shows that on the CPU for
+bf16, fp16 and tf32).  The reference widens every fp32 operand to double
+exactly (modules/tensor/operators.cpp:757-766), so any narrower operand path
+fails them.
 """
 import ctypes as C
 
@@ -40,6 +52,38 @@ EXACT = 2.0 ** 24
 def ints(seed, shape, lo=-2, hi=2):
     """Integers in [lo, hi] as fp32 (seeded)."""
     return np.random.default_rng(seed).integers(lo, hi + 1, size=shape).astype(F)
+
+
+WIDE = 4095
+
+
+def wide(seed, shape, lo=-WIDE, hi=WIDE):
+    """Integers with up to 12 significant bits as fp32 (seeded)."""
+    return ints(seed, shape, lo, hi)
+
+
+def ternary(seed, shape, k_axis, nnz=4000):
+    """Signs +-1 at exactly min(nnz, K) positions of every k-vector along
+    k_axis, 0 elsewhere (seeded).  With |a| <= 4095 on the other side and nnz
+    <= 4095, every dot product keeps sum |a||b| + 4095 < 2**24."""
+    rng = np.random.default_rng(seed)
+    keys = rng.random(shape)
+    K = shape[k_axis]
+    take = min(nnz, K)
+    if take == K:
+        mask = np.ones(shape, bool)
+    else:
+        kth = np.partition(keys, take - 1, axis=k_axis).take([take - 1], axis=k_axis)
+        mask = keys <= kth
+    sign = rng.integers(0, 2, size=shape).astype(F) * 2 - 1
+    return (sign * mask).astype(F)
+
+
+def wide_pair(seed, a_shape, b_shape, wide_side, nnz=4000):
+    """(A, B) for C = A.B with the wide operand on wide_side ("A" or "B")."""
+    if wide_side == "A":
+        return wide(seed, a_shape), ternary(seed + 1, b_shape, 0, nnz)
+    return ternary(seed, a_shape, 1, nnz), wide(seed + 1, b_shape)
 
 
 def relu32(y):
@@ -156,6 +200,19 @@ def test_sgemm_integer_operands_are_exact_at_full_size(M, N, Kd, epi, path):
         assert_bits(ref, want[:r], "oracle slab")
 
 
+@pytest.mark.parametrize("wide_side", ["A", "B"])
+@pytest.mark.parametrize("M,N,Kd,epi,path", GEMM_SHAPES, ids=[s[4].split(":")[0] for s in GEMM_SHAPES])
+def test_sgemm_wide_operands_stay_fp32(M, N, Kd, epi, path, wide_side):
+    # One operand wide (12-bit integers), the other ternary: bit-exact only
+    # if neither operand is narrowed on its way into the MFMA (or FMA).
+    print(f"wide sgemm {M}x{N}x{Kd} epi={epi} wide {wide_side} ({path})", flush=True)
+    seed = 0xB000 + M * 131 + N * 7 + Kd
+    a, b = wide_pair(seed, (M, Kd), (Kd, N), wide_side)
+    bias = wide(seed + 2, (N,)) if epi & H.EPI_BIAS else None
+    want = exact_dense(a, b, bias, bool(epi & H.EPI_RELU))
+    assert_bits(K.sgemm(a, b, bias, epi), want, f"{path}, wide {wide_side}")
+
+
 def test_sgemm_exact_results_repeat_across_calls():
     # Split partial scratch reused by a second, smaller call (skinny and tiles).
     for M, N, Kd in ((16, 4096, 4096), (16, 1024, 8192), (512, 128, 9216), (200, 72, 1000)):
@@ -250,6 +307,27 @@ def test_conv2d_integer_operands_are_exact_at_full_size(geom, rng_, path):
     x = ints(seed, (N, Cin, H_, W_), *rng_)
     w = ints(seed + 1, (Co, Cin, kh, kw), *rng_)
     b = ints(seed + 2, (Co,), *rng_)
+    _conv_every_mode_is_exact(x, w, b, geom, path)
+
+
+@pytest.mark.parametrize("wide_side", ["x", "w"])
+@pytest.mark.parametrize("geom,rng_,path", CONV_CASES, ids=[c[2].split(":")[0] for c in CONV_CASES])
+def test_conv2d_wide_operands_stay_fp32(geom, rng_, path, wide_side):
+    # One of x and w wide (12-bit integers), the other in {-1, 0, 1}; the
+    # GEMM views K = C*KH*KW <= 576, so sum |x||w| + |b| < 2**24.
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
+    print(f"wide conv2d {geom} wide {wide_side} ({path})", flush=True)
+    seed = 0xC000 + N * 1000 + Cin * 10 + Co
+    if wide_side == "x":
+        x, w = wide(seed, (N, Cin, H_, W_)), ints(seed + 1, (Co, Cin, kh, kw), -1, 1)
+    else:
+        x, w = ints(seed, (N, Cin, H_, W_), -1, 1), wide(seed + 1, (Co, Cin, kh, kw))
+    b = wide(seed + 2, (Co,))
+    _conv_every_mode_is_exact(x, w, b, geom, f"{path}, wide {wide_side}")
+
+
+def _conv_every_mode_is_exact(x, w, b, geom, path):
+    N, Cin, H_, W_, Co, kh, kw, stride, pad = geom
     epi = H.EPI_BIAS | H.EPI_RELU
     want = exact_conv(x, w, b, stride, pad, relu=True)
     assert_bits(_conv(x, w, b, geom, epi), want, path)
@@ -372,3 +450,163 @@ def test_skinny_split_sums_are_exact_on_every_call(M, N, Kd):
         H.call("camel_hip_sgemm", P(da.ptr), P(db.ptr), P(dc.ptr), M, N, Kd, P(dbias.ptr),
                H.EPI_BIAS | H.EPI_RELU)
         assert_bits(K.host(dc, F, (M, N)), want, f"call {i}")
+
+
+# ----------------------------------------- fused paths with wide operands
+# Each case makes one operand of one layer wide (12-bit integers, or the wide
+# activations a wide layer produces) and keeps every other operand ternary
+# and sparse enough that every layer's sum |a||b| + |bias| < 2**24
+# (exact_dense / exact_conv assert it), so each layer's operands are pinned
+# to fp32 in turn.
+
+def _conv_w(seed, co, c, k, nnz):
+    """Ternary conv weights with exactly min(nnz, c*k*k) nonzeros per output channel."""
+    return ternary(seed, (co, c * k * k), 1, nnz).reshape(co, c, k, k)
+
+
+HEAD_WIDE = {
+    # x, w1, w2 generators for the CNN head 512x9216 -> 128 (relu) -> 10
+    "x": lambda s: (wide(s, (512, 9216)), ternary(s + 1, (9216, 128), 0, 4),
+                    ternary(s + 3, (128, 10), 0, 128)),
+    "w1": lambda s: (ternary(s, (512, 9216), 1, 40), wide(s + 1, (9216, 128)),
+                     ternary(s + 3, (128, 10), 0, 64)),
+    "w2": lambda s: (ternary(s, (512, 9216), 1, 4), ternary(s + 1, (9216, 128), 0, 4000),
+                     wide(s + 3, (128, 10))),
+}
+
+
+@pytest.mark.parametrize("which", sorted(HEAD_WIDE))
+def test_dense_head_wide_operands_stay_fp32(which):
+    # camel_hip_dense_head on 16 split partials: layer 1's A or B wide, or
+    # layer 2's B wide (layer 2's A, the split sums, is wide in the first two).
+    s = 0xD000 + len(which)
+    x, w1, w2 = HEAD_WIDE[which](s)
+    b1 = ints(s + 2, (128,), -1, 1)
+    b2 = wide(s + 4, (10,))
+    epi = H.EPI_BIAS | H.EPI_RELU
+    h = exact_dense(x, w1, b1, True)
+    logits = exact_dense(h, w2, b2, False)
+    assert_bits(_dense_head(x, w1, b1, w2, b2, epi, H.EPI_BIAS, 0), logits, f"head, wide {which}")
+
+
+@pytest.mark.parametrize("wide_side", ["A", "B"])
+def test_dense_softmax_wide_operands_stay_fp32(wide_side):
+    # MLP layer 3 + softmax fused (1024 x 1024 -> 10): the softmax of the
+    # exact logits within the softmax bar.  The logits of wide operands are
+    # large, so most rows are near one-hot; the bar still holds per element.
+    x, w = wide_pair(0xD100, (1024, 1024), (1024, 10), wide_side)
+    b = wide(0xD102, (10,))
+    logits = exact_dense(x, w, b, False)
+    dx, dw, db = K.dev(x), K.dev(w), K.dev(b)
+    dy = K.empty(1024 * 10 * 4)
+    H.call("camel_hip_dense_softmax", P(dx.ptr), P(dw.ptr), P(db.ptr), P(dy.ptr), 1024, 10, 1024,
+           H.EPI_BIAS)
+    softmax_close(K.host(dy, F, (1024, 10)), logits)
+    # the logits alone through the thin kernel, bit for bit
+    assert_bits(K.sgemm(x, w, b, H.EPI_BIAS), logits, f"classifier, wide {wide_side}")
+
+
+CONV2_WIDE = {
+    # x (conv2's input, NCHW4), w: conv2 of the CNN, 512x32x26x26 -> 64, pooled
+    "x": lambda s: (wide(s, (512, 32, 26, 26), 0, WIDE), _conv_w(s + 1, 64, 32, 3, 288)),
+    "w": lambda s: (ints(s, (512, 32, 26, 26), 0, 1), wide(s + 1, (64, 32, 3, 3))),
+}
+
+
+@pytest.mark.parametrize("which", sorted(CONV2_WIDE))
+def test_cnn_pooled_conv2_wide_operands_stay_fp32(which):
+    geom = (512, 32, 26, 26, 64, 3, 3, 1, 0)
+    x, w = CONV2_WIDE[which](0xD200 + len(which))
+    b = wide(0xD202, (64,))
+    want = pool2(exact_conv(x, w, b, 1, 0, relu=True))
+    wp = np.ascontiguousarray(w.transpose(0, 2, 3, 1))
+    flags = H.EPI_BIAS | H.EPI_RELU | H.CONV_X_NCHW4 | H.CONV_W_PACKED
+    assert_bits(_conv(x, wp, b, geom, flags, pooled=True, x_layout="nchw4"), want,
+                f"pooled conv2, wide {which}")
+
+
+PAIR_WIDE = {
+    # x, w1, w2 of the fused conv pair (512x1x28x28 -> 32 -> 64, pooled):
+    # wide pixels make conv1's output (conv2's B operand) wide; wide w2 is
+    # conv2's A operand.
+    "x": lambda s: (wide(s, (512, 1, 28, 28)), ints(s + 1, (32, 1, 3, 3), -1, 1),
+                    ints(s + 3, (64, 32, 3, 3), -1, 1)),
+    "w2": lambda s: (ints(s, (512, 1, 28, 28), 0, 1), ints(s + 1, (32, 1, 3, 3), -1, 1),
+                     wide(s + 3, (64, 32, 3, 3))),
+}
+
+
+@pytest.mark.parametrize("which", sorted(PAIR_WIDE))
+def test_conv_pair_pool_wide_operands_stay_fp32(which):
+    s = 0xD300 + len(which)
+    x, w1, w2 = PAIR_WIDE[which](s)
+    b1, b2 = ints(s + 2, (32,), -1, 1), wide(s + 4, (64,))
+    want = pool2(exact_conv(exact_conv(x, w1, b1, relu=True), w2, b2, relu=True))
+    dx, dw1, db1, dw2, db2 = K.dev(x), K.dev(w1), K.dev(b1), K.dev(w2), K.dev(b2)
+    dy = K.empty(want.nbytes)
+    epi = H.EPI_BIAS | H.EPI_RELU
+    H.call("camel_hip_conv2d_pair_pool2", P(dx.ptr), P(dw1.ptr), P(db1.ptr), P(dw2.ptr),
+           P(db2.ptr), P(dy.ptr), 512, 28, 28, 32, 64, epi, epi)
+    assert_bits(K.host(dy, F, want.shape), want, f"conv pair, wide {which}")
+
+
+MLP_WIDE = {
+    # x, W1, W2, W3 for 1024 x 784 -> 1024 -> 1024 -> 10 (relu, relu, logits)
+    # wide activations all the way (layer 1's A, then layers 2 and 3 see
+    # 15- and 24-bit activations)
+    "x": lambda s: (wide(s, (1024, 784)), ternary(s + 1, (784, 1024), 0, 4),
+                    ternary(s + 2, (1024, 1024), 0, 512), ternary(s + 3, (1024, 10), 0, 1)),
+    # layer 1's weights wide
+    "w1": lambda s: (ints(s, (1024, 784), 0, 1) * ternary(s + 9, (1024, 784), 1, 4) ** 2,
+                     wide(s + 1, (784, 1024)), ternary(s + 2, (1024, 1024), 0, 512),
+                     ternary(s + 3, (1024, 10), 0, 1)),
+    # layer 2's weights wide (its input has entries in {0, 1, 2})
+    "w2": lambda s: (ints(s, (1024, 784), 0, 1) * ternary(s + 9, (1024, 784), 1, 2) ** 2,
+                     ternary(s + 1, (784, 1024), 0, 784), wide(s + 2, (1024, 1024)),
+                     ternary(s + 3, (1024, 10), 0, 1)),
+}
+
+
+@pytest.mark.parametrize("which", sorted(MLP_WIDE))
+def test_mlp_chain_wide_operands_stay_fp32(which, _release):
+    # BASELINE config 2's shapes through the fused chain, the logits bit for
+    # bit, with one layer's operands wide in turn.
+    s = 0xD400 + 16 * len(which)
+    x, *wn = MLP_WIDE[which](s)
+    bn = [ints(s + 5, (1024,), -1, 1), ints(s + 6, (1024,), -1, 1), wide(s + 7, (10,))]
+    h = exact_dense(x, wn[0], bn[0], True)
+    h = exact_dense(h, wn[1], bn[1], True)
+    logits = exact_dense(h, wn[2], bn[2], False)
+    ws, bs = [t(w) for w in wn], [t(b) for b in bn]
+    head = T.Chain(("dense_relu", ws[0], bs[0]), ("dense_relu", ws[1], bs[1]), ("dense", ws[2], bs[2]))
+    assert_bits(head(t(x)).numpy(), logits, f"MLP logits, wide {which}")
+    head.release()
+
+
+CNN_WIDE = {
+    # x, w1, w2, w3, w4: wide pixels (conv2's B and dense1's A wide), or wide
+    # conv2 weights (conv2's A wide, dense1's A wide)
+    "x": lambda s: (wide(s, (512, 1, 28, 28)), ints(s + 1, (32, 1, 3, 3), -1, 1),
+                    ints(s + 2, (64, 32, 3, 3), -1, 1), ternary(s + 3, (9216, 128), 0, 1),
+                    ternary(s + 4, (128, 10), 0, 1)),
+    "w2": lambda s: (ints(s, (512, 1, 28, 28), 0, 1), ints(s + 1, (32, 1, 3, 3), -1, 1),
+                     wide(s + 2, (64, 32, 3, 3)), ternary(s + 3, (9216, 128), 0, 1),
+                     ternary(s + 4, (128, 10), 0, 1)),
+}
+
+
+@pytest.mark.parametrize("which", sorted(CNN_WIDE))
+def test_cnn_chain_wide_operands_stay_fp32(which, _release):
+    s = 0xD500 + 16 * len(which)
+    x, w1, w2, w3, w4 = CNN_WIDE[which](s)
+    b1, b2 = ints(s + 5, (32,), -1, 1), ints(s + 6, (64,), -1, 1)
+    b3, b4 = ints(s + 7, (128,), -1, 1), wide(s + 8, (10,))
+    h = exact_conv(x, w1, b1, relu=True)
+    h = pool2(exact_conv(h, w2, b2, relu=True)).reshape(512, 9216)
+    h = exact_dense(h, w3, b3, True)
+    logits = exact_dense(h, w4, b4, False)
+    tw = [t(a) for a in (w1, b1, w2, b2, w3, b3, w4, b4)]
+    head = T.Chain(("conv2d_relu", tw[0], tw[1]), ("conv2d_relu", tw[2], tw[3]), ("maxpool2d", 2, 2),
+                   ("reshape", 512, 9216), ("dense_relu", tw[4], tw[5]), ("dense", tw[6], tw[7]))
+    assert_bits(head(t(x)).numpy(), logits, f"CNN logits, wide {which}")
+    head.release()

@@ -13,7 +13,7 @@ from camel_amd import datagen as D
 from camel_amd import tensor as T
 from oracle import ffi as O
 from tests import hipkit as K
-from tests.test_gpu_exact import assert_bits, exact_dense, ints
+from tests.test_gpu_exact import assert_bits, exact_dense, ints, wide, wide_pair
 
 pytestmark = pytest.mark.gpu
 
@@ -56,6 +56,20 @@ def test_transposed_a_gemm_is_exact(M, N, Kd, epi, path):
     want = exact_dense(a, b, bias, bool(epi & H.EPI_RELU))
     got = sgemm_at(np.ascontiguousarray(a.T), b, bias, epi)
     assert_bits(got, want, path)
+
+
+@pytest.mark.parametrize("wide_side", ["A", "B"])
+@pytest.mark.parametrize("M,N,Kd,epi,path", TN_SHAPES, ids=[s[4].split(":")[0] for s in TN_SHAPES])
+def test_transposed_a_gemm_wide_operands_stay_fp32(M, N, Kd, epi, path, wide_side):
+    # One operand wide (12-bit integers), the other ternary: the transposed
+    # loaders must hand the MFMA fp32 operands (see tests/test_gpu_exact.py).
+    print(f"wide TN sgemm {M}x{N}x{Kd} wide {wide_side} ({path})", flush=True)
+    seed = 0xE000 + M + N + Kd
+    a, b = wide_pair(seed, (M, Kd), (Kd, N), wide_side)
+    bias = wide(seed + 2, (N,)) if epi & H.EPI_BIAS else None
+    want = exact_dense(a, b, bias, bool(epi & H.EPI_RELU))
+    got = sgemm_at(np.ascontiguousarray(a.T), b, bias, epi)
+    assert_bits(got, want, f"{path}, wide {wide_side}")
 
 
 def test_transposed_a_gemm_matches_the_oracle_on_real_values():
