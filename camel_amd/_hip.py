@@ -54,6 +54,7 @@ _SIGNATURES = {
     "camel_hip_stream": [],
     "camel_hip_malloc": [C.POINTER(_P), C.c_size_t],
     "camel_hip_free": [_P],
+    "camel_hip_free_shared": [_P],
     "camel_hip_pool_trim": [],
     "camel_hip_pool_stats": [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)],
     "camel_hip_h2d": [_P, _P, C.c_size_t],

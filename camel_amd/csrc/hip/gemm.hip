@@ -172,6 +172,15 @@ __device__ __forceinline__ size_t conv_out_off(const GemmArgs &g, bool q4, int i
 // and keeps each aligned run of 8 columns (one 8-lane operand read) whole.
 __device__ __forceinline__ int b_slot(int n) { return n ^ ((n >> 3) & 3); }
 
+// Address of row k of a row-major operand with leading dimension ld, computed
+// as an integer: k is below 0 for a ragged first stage, whose rows are never
+// read (the loaders' guards), and no pointer outside the operand is formed by
+// pointer arithmetic.
+__device__ __forceinline__ const float *row_address(const float *base, int k, int ld) {
+    return reinterpret_cast<const float *>(reinterpret_cast<uintptr_t>(base) +
+                                           (size_t)k * ld * sizeof(float));
+}
+
 // Logical tile id -> (tm, tn), grouped GROUP_M tile-rows deep so that
 // consecutive ids share B panels.  A bijection on [0, tiles_m * tiles_n).
 __device__ __forceinline__ void tile_of(int id, int tiles_m, int tiles_n, int &tm, int &tn) {
@@ -355,13 +364,17 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int gk = k0 + 4 * kq + u;
-                const float *row = g.A + (size_t)gk * g.lda;
+                // gk is below 0 in a ragged first stage: the row is an offset
+                // (it wraps) or an address computed as an integer, and a
+                // pointer into A is formed only where the guard admits a load
                 if constexpr (AMODE == LOAD_TVEC) {
+                    const size_t row = (size_t)gk * g.lda;
                     const int gm = m0 + 4 * mq;
                     rat[i][u] = (FULL || (gm < g.M && gk >= 0 && gk < kend))
-                                    ? *reinterpret_cast<const float4 *>(row + gm)
+                                    ? *reinterpret_cast<const float4 *>(g.A + (row + gm))
                                     : make_float4(0.f, 0.f, 0.f, 0.f);
                 } else {
+                    const float *row = row_address(g.A, gk, g.lda);
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
@@ -378,17 +391,17 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             if (A_TAIL && q >= T::A_TOTAL) break;
             const int kq = q % T::KQ, m = q / T::KQ;
             const int gm = m0 + m, gk = k0 + 4 * kq;
-            const float *src = g.A + (size_t)gm * g.lda + gk;
+            const size_t src = (size_t)gm * g.lda + gk;
             if constexpr (AMODE == LOAD_VEC) {
                 ra[i] = (FULL || (gm < g.M && gk >= 0 && gk < kend))
-                            ? *reinterpret_cast<const float4 *>(src)
-                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+                            ? *reinterpret_cast<const float4 *>(g.A + src)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
                 const bool rv = FULL || gm < g.M;
-                ra[i].x = (rv && (FULL || (gk + 0 >= 0 && gk + 0 < kend))) ? src[0] : 0.f;
-                ra[i].y = (rv && (FULL || (gk + 1 >= 0 && gk + 1 < kend))) ? src[1] : 0.f;
-                ra[i].z = (rv && (FULL || (gk + 2 >= 0 && gk + 2 < kend))) ? src[2] : 0.f;
-                ra[i].w = (rv && (FULL || (gk + 3 >= 0 && gk + 3 < kend))) ? src[3] : 0.f;
+                ra[i].x = (rv && (FULL || (gk + 0 >= 0 && gk + 0 < kend))) ? g.A[src + 0] : 0.f;
+                ra[i].y = (rv && (FULL || (gk + 1 >= 0 && gk + 1 < kend))) ? g.A[src + 1] : 0.f;
+                ra[i].z = (rv && (FULL || (gk + 2 >= 0 && gk + 2 < kend))) ? g.A[src + 2] : 0.f;
+                ra[i].w = (rv && (FULL || (gk + 3 >= 0 && gk + 3 < kend))) ? g.A[src + 3] : 0.f;
             }
         }
         if constexpr (is_nhwc<BMODE> && LB) {
@@ -401,13 +414,16 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 const int ih = px_ih[i] + kh, iw = px_iw[i] + kw;
                 const bool in = (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W &&
                                 (FULL || k0 < kend);
-                const float *src = g.B + (size_t)(px_base[i] + koff);
+                // a padding pixel's offset is below 0: formed into a pointer
+                // only when the pixel is in the image
+                const size_t src = (size_t)(px_base[i] + koff);
                 if constexpr (is_planes<BMODE>) {
-                    rbn[i] = in ? make_float4(src[0], src[g.chs], src[2 * (size_t)g.chs],
-                                              src[3 * (size_t)g.chs])
+                    rbn[i] = in ? make_float4(g.B[src], g.B[src + g.chs],
+                                              g.B[src + 2 * (size_t)g.chs],
+                                              g.B[src + 3 * (size_t)g.chs])
                                 : make_float4(0.f, 0.f, 0.f, 0.f);
                 } else {
-                    rbn[i] = in ? *reinterpret_cast<const float4 *>(src)
+                    rbn[i] = in ? *reinterpret_cast<const float4 *>(g.B + src)
                                 : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
@@ -423,10 +439,12 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
                     const ptrdiff_t back = again ? (ptrdiff_t)T::BK * g.ldb : 0;
-                    const float *src = B_PTR ? g.B + (b_vec_off[i] - back + (ptrdiff_t)u * g.ldb)
-                                             : g.B + (size_t)gk * g.ldb + gn;
+                    // an offset (it wraps below 0 for the ragged first stage,
+                    // where the guard keeps it from becoming a pointer)
+                    const size_t src = B_PTR ? (size_t)(b_vec_off[i] - back + (ptrdiff_t)u * g.ldb)
+                                             : (size_t)gk * g.ldb + gn;
                     rb[i][u] = (FULL || (gn < g.N && gk >= 0 && gk < kend))
-                                   ? *reinterpret_cast<const float4 *>(src)
+                                   ? *reinterpret_cast<const float4 *>(g.B + src)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
                 if constexpr (B_PTR) b_vec_off[i] += again ? 0 : (ptrdiff_t)T::BK * g.ldb;
@@ -434,7 +452,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int gk = k0 + 4 * kq + u;
-                    const float *row = g.B + (size_t)gk * g.ldb;
+                    const float *row = row_address(g.B, gk, g.ldb);
                     float v[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {

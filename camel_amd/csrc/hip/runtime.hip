@@ -2,6 +2,7 @@
 // pooled device allocator, boundary copies, events and the creation kernels.
 #include "common.h"
 
+#include <cstdio>
 #include <cstring>
 #include <unordered_map>
 #include <vector>
@@ -21,6 +22,11 @@ struct State {
     // Pool: exact-size free lists over rounded sizes; blocks never shrink.
     std::unordered_map<size_t, std::vector<void *>> free_lists;
     std::unordered_map<void *, size_t> live;
+    // Blocks released while a consumer may still read them on its own
+    // streams (zero-copy DLPack exports): held back from the free lists until
+    // a device-wide synchronisation has completed (drain_deferred).
+    std::vector<std::pair<void *, size_t>> deferred;
+    bool deferred_warned = false;
     size_t in_use = 0;
     size_t cached = 0;
 };
@@ -119,6 +125,33 @@ int init_device(int device) {
     s.device = device;
     s.initialised = true;
     return clear_error_flag();
+}
+
+// Returns the deferred blocks to the free lists once every stream of the
+// device has drained.  A release never synchronises by itself (it may run in
+// a garbage collector, or while another library captures a graph, where a
+// device-wide wait fails); the wait happens here, at the library's own
+// allocation misses and synchronisation points, and a failed wait keeps the
+// blocks deferred for the next attempt.
+void drain_deferred() {
+    State &s = state();
+    if (s.deferred.empty()) return;
+    if (hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        if (!s.deferred_warned) {
+            std::fprintf(stderr, "camel_hip: %zu exported block(s) held back: the device-wide "
+                                 "wait before their reuse failed; retrying later\n",
+                         s.deferred.size());
+            s.deferred_warned = true;
+        }
+        return;
+    }
+    for (const auto &[ptr, size] : s.deferred) {
+        s.in_use -= size;
+        s.free_lists[size].push_back(ptr);
+        s.cached += size;
+    }
+    s.deferred.clear();
 }
 
 } // namespace
@@ -220,6 +253,7 @@ int camel_hip_device_sync(void) {
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
     CAMEL_RETURN_IF(check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize"));
+    drain_deferred();
     return ok();
 }
 
@@ -249,6 +283,16 @@ int camel_hip_malloc(void **ptr, size_t bytes) {
         it->second.pop_back();
         s.cached -= size;
     } else {
+        drain_deferred();
+        auto again = s.free_lists.find(size);
+        if (again != s.free_lists.end() && !again->second.empty()) {
+            *ptr = again->second.back();
+            again->second.pop_back();
+            s.cached -= size;
+            s.live[*ptr] = size;
+            s.in_use += size;
+            return ok();
+        }
         void *p = nullptr;
         hipError_t err = hipMalloc(&p, size);
         if (err != hipSuccess) {
@@ -285,10 +329,23 @@ int camel_hip_free(void *ptr) {
     return ok();
 }
 
+int camel_hip_free_shared(void *ptr) {
+    if (!ptr) return ok();
+    CAMEL_LOCK();
+    State &s = state();
+    auto it = s.live.find(ptr);
+    if (it == s.live.end()) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_free_shared: unknown pointer");
+    // Still counted in use until drain_deferred returns it to the pool.
+    s.deferred.emplace_back(ptr, it->second);
+    s.live.erase(it);
+    return ok();
+}
+
 int camel_hip_pool_trim(void) {
     CAMEL_LOCK();
     State &s = state();
     if (!s.initialised) return ok();
+    drain_deferred();
     CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize"));
     for (auto &kv : s.free_lists) {
         for (void *p : kv.second) (void)hipFree(p);

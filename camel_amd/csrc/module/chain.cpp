@@ -257,9 +257,9 @@ std::vector<LayerChain::Group> LayerChain::schedule(std::span<const int64_t> sha
     return groups;
 }
 
-std::string LayerChain::plan(std::span<const int64_t> shape) const {
+std::string LayerChain::plan(std::span<const int64_t> shape, TypeCode dtype) const {
     std::ostringstream out;
-    for (const Group &g : schedule(shape)) {
+    for (const Group &g : schedule(shape, dtype)) {
         const LayerStep &s = *g.step;
         switch (g.kind) {
         case Group::Dense:

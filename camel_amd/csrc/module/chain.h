@@ -66,9 +66,9 @@ public:
     // x -> chain: a new device tensor.  Throws with the failing layer's error
     // text.
     TensorObject *apply(const TensorObject *x) const;
-    // The kernel groups apply would run for an input of this shape, one per
-    // line (e.g. "conv2d_relu+maxpool2d(2,2) x=nchw4").
-    std::string plan(std::span<const int64_t> shape) const;
+    // The kernel groups apply would run for an input of this shape and
+    // dtype, one per line (e.g. "conv2d_relu+maxpool2d(2,2) x=nchw4").
+    std::string plan(std::span<const int64_t> shape, TypeCode dtype = TypeCode::Float32) const;
     size_t size() const { return steps_.size(); }
 
 private:

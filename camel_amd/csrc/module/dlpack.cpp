@@ -4,9 +4,8 @@
 // Here a tensor can also be exported without a copy from HBM (kDLROCM): the
 // managed tensor holds a reference to the payload's Storage, so the device
 // block outlives the tensor handle until the consumer's deleter runs, and the
-// Storage is marked shared, so its release waits for every stream of the
-// device before the block can be reused (the consumer reads it on its own
-// streams).  Imports
+// Storage is marked shared, so its block is reused only after a later
+// device-wide wait (the consumer reads it on its own streams).  Imports
 // copy, from host memory or from device memory on the library's device.
 #include "tensor_object.h"
 

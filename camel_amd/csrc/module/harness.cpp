@@ -429,12 +429,16 @@ int camel_chain_apply(uint64_t chain, uint64_t x, uint64_t *result) {
     });
 }
 
-int camel_chain_plan(uint64_t chain, int64_t rank, const int64_t *shape, char *buf, size_t cap,
-                     size_t *needed) {
+int camel_chain_plan(uint64_t chain, int64_t rank, const int64_t *shape, uint32_t dtype, char *buf,
+                     size_t cap, size_t *needed) {
     LayerChain *c = chainOf(chain);
     if (!c || rank < 0 || (rank > 0 && !shape))
         return fail(CAMEL_TENSOR_ERR_ARG, "camel_chain_plan: bad arguments");
-    const std::string text = c->plan(std::span<const int64_t>(shape, (size_t)rank));
+    if (dtype != CAMEL_TC_FLOAT32 && dtype != CAMEL_TC_INT64 && dtype != CAMEL_TC_BOOL &&
+        dtype != CAMEL_TC_FLOAT64 && dtype != CAMEL_TC_INT32)
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_chain_plan: not a tensor dtype");
+    const std::string text = c->plan(std::span<const int64_t>(shape, (size_t)rank),
+                                     normalizeTensorDType(static_cast<TypeCode>(dtype)));
     if (needed) *needed = text.size() + 1;
     if (buf && cap > 0) {
         const size_t n = std::min(cap - 1, text.size());

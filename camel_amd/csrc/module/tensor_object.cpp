@@ -10,7 +10,7 @@
 #include <iomanip>
 #include <iostream>
 #include <sstream>
-#include <unordered_set>
+#include <unordered_map>
 
 namespace camel_amd::tensor {
 
@@ -22,10 +22,13 @@ void checkHip(int status) {
 
 Storage::~Storage() {
     if (!dev) return;
-    // A destructor cannot report an error; a failed wait leaves the block
-    // out of the pool rather than risking its reuse under a live reader.
-    if (shared && camel_hip_device_sync() != 0) return;
-    camel_hip_free(dev);
+    // A shared block's last reader may be a consumer's stream: the shim holds
+    // it back until a device-wide wait, without waiting here (this may run in
+    // a consumer's garbage collector).
+    if (shared)
+        camel_hip_free_shared(dev);
+    else
+        camel_hip_free(dev);
 }
 
 namespace {
@@ -646,35 +649,69 @@ TensorObject *tensorFromArray(slot_t slot, TypeCode valueCode) {
 // ---- lifetime registry ----------------------------------------------------------
 
 namespace {
+// Each registered object carries a serial number, so a record of an object
+// that was released (and whose address a new object may have taken since)
+// never matches the new one.
 struct Registry {
     std::mutex mutex;
-    std::unordered_set<TensorObject *> tensors;
-    std::unordered_set<ArrayObject *> arrays;
+    uint64_t next = 1;
+    std::unordered_map<TensorObject *, uint64_t> tensors;
+    std::unordered_map<ArrayObject *, uint64_t> arrays;
 };
 Registry &registry() {
     static Registry *r = new Registry(); // never destroyed: tensors may outlive static teardown
     return *r;
 }
+
+template <class Obj>
+bool eraseIf(std::unordered_map<Obj *, uint64_t> &live, Obj *obj, uint64_t serial) {
+    auto it = live.find(obj);
+    if (it == live.end() || (serial != 0 && it->second != serial)) return false;
+    live.erase(it);
+    return true;
+}
 } // namespace
 
 void registerObject(TensorObject *t) {
+    uint64_t serial;
     {
         std::lock_guard<std::mutex> lock(registry().mutex);
-        registry().tensors.insert(t);
+        serial = registry().next++;
+        registry().tensors[t] = serial;
     }
-    CreationScope::record(t);
+    CreationScope::record(t, serial);
 }
 
 void registerObject(ArrayObject *a) {
+    uint64_t serial;
     {
         std::lock_guard<std::mutex> lock(registry().mutex);
-        registry().arrays.insert(a);
+        serial = registry().next++;
+        registry().arrays[a] = serial;
     }
-    CreationScope::record(a);
+    CreationScope::record(a, serial);
 }
 
 namespace {
 thread_local CreationScope *t_scope = nullptr;
+
+bool releaseTensorSerial(TensorObject *t, uint64_t serial) {
+    {
+        std::lock_guard<std::mutex> lock(registry().mutex);
+        if (!eraseIf(registry().tensors, t, serial)) return false;
+    }
+    delete t;
+    return true;
+}
+
+bool releaseArraySerial(ArrayObject *a, uint64_t serial) {
+    {
+        std::lock_guard<std::mutex> lock(registry().mutex);
+        if (!eraseIf(registry().arrays, a, serial)) return false;
+    }
+    delete a;
+    return true;
+}
 } // namespace
 
 CreationScope::CreationScope() : parent_(t_scope), uncaught_(std::uncaught_exceptions()) {
@@ -684,40 +721,28 @@ CreationScope::CreationScope() : parent_(t_scope), uncaught_(std::uncaught_excep
 CreationScope::~CreationScope() {
     t_scope = parent_;
     if (std::uncaught_exceptions() > uncaught_) {
-        // releaseTensor / releaseArray skip objects already released.
-        for (TensorObject *t : tensors_) releaseTensor(t);
-        for (ArrayObject *a : arrays_) releaseArray(a);
+        // Objects released meanwhile (an operator's freed temporaries) fail
+        // the serial check, also when another thread's new object now has
+        // the same address.
+        for (const auto &[t, serial] : tensors_) releaseTensorSerial(t, serial);
+        for (const auto &[a, serial] : arrays_) releaseArraySerial(a, serial);
     } else if (parent_) {
         parent_->tensors_.insert(parent_->tensors_.end(), tensors_.begin(), tensors_.end());
         parent_->arrays_.insert(parent_->arrays_.end(), arrays_.begin(), arrays_.end());
     }
 }
 
-void CreationScope::record(TensorObject *t) {
-    if (t_scope) t_scope->tensors_.push_back(t);
+void CreationScope::record(TensorObject *t, uint64_t serial) {
+    if (t_scope) t_scope->tensors_.emplace_back(t, serial);
 }
 
-void CreationScope::record(ArrayObject *a) {
-    if (t_scope) t_scope->arrays_.push_back(a);
+void CreationScope::record(ArrayObject *a, uint64_t serial) {
+    if (t_scope) t_scope->arrays_.emplace_back(a, serial);
 }
 
-bool releaseTensor(TensorObject *t) {
-    {
-        std::lock_guard<std::mutex> lock(registry().mutex);
-        if (registry().tensors.erase(t) == 0) return false;
-    }
-    delete t;
-    return true;
-}
+bool releaseTensor(TensorObject *t) { return releaseTensorSerial(t, 0); }
 
-bool releaseArray(ArrayObject *a) {
-    {
-        std::lock_guard<std::mutex> lock(registry().mutex);
-        if (registry().arrays.erase(a) == 0) return false;
-    }
-    delete a;
-    return true;
-}
+bool releaseArray(ArrayObject *a) { return releaseArraySerial(a, 0); }
 
 bool isLiveTensor(const TensorObject *t) {
     std::lock_guard<std::mutex> lock(registry().mutex);
@@ -735,15 +760,15 @@ size_t liveTensorCount() {
 }
 
 size_t releaseAll() {
-    std::unordered_set<TensorObject *> tensors;
-    std::unordered_set<ArrayObject *> arrays;
+    std::unordered_map<TensorObject *, uint64_t> tensors;
+    std::unordered_map<ArrayObject *, uint64_t> arrays;
     {
         std::lock_guard<std::mutex> lock(registry().mutex);
         tensors.swap(registry().tensors);
         arrays.swap(registry().arrays);
     }
-    for (TensorObject *t : tensors) delete t;
-    for (ArrayObject *a : arrays) delete a;
+    for (const auto &entry : tensors) delete entry.first;
+    for (const auto &entry : arrays) delete entry.first;
     return tensors.size() + arrays.size();
 }
 

@@ -25,6 +25,7 @@
 #include <memory>
 #include <mutex>
 #include <span>
+#include <utility>
 #include <vector>
 
 namespace camel_amd::tensor {
@@ -52,8 +53,8 @@ struct Storage {
     bool hostValid = false;
     // Set when the device block was handed out without a copy (DLPack
     // export): a consumer may still read it on its own stream when the last
-    // reference goes, so the release waits for the whole device before the
-    // block returns to the pool, where the library stream could reuse it.
+    // reference goes, so the block returns to the pool, where the library
+    // stream could reuse it, only after a later device-wide wait.
     bool shared = false;
     std::mutex mutex; // residency transitions may race under a thread-pool scheduler
 };
@@ -195,15 +196,16 @@ class CreationScope {
     CreationScope(const CreationScope &) = delete;
     CreationScope &operator=(const CreationScope &) = delete;
 
-    // Records a new object in the innermost active scope of this thread.
-    static void record(TensorObject *t);
-    static void record(ArrayObject *a);
+    // Records a new object (with its registry serial number) in the
+    // innermost active scope of this thread.
+    static void record(TensorObject *t, uint64_t serial);
+    static void record(ArrayObject *a, uint64_t serial);
 
   private:
     CreationScope *parent_;
     int uncaught_;
-    std::vector<TensorObject *> tensors_;
-    std::vector<ArrayObject *> arrays_;
+    std::vector<std::pair<TensorObject *, uint64_t>> tensors_;
+    std::vector<std::pair<ArrayObject *, uint64_t>> arrays_;
 };
 
 } // namespace camel_amd::tensor

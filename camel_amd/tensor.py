@@ -104,7 +104,7 @@ _SIG = {
     "camel_chain_create": ([C.POINTER(_U64)], C.c_int),
     "camel_chain_append": ([_U64, C.c_char_p, _I64, C.POINTER(Value)], C.c_int),
     "camel_chain_apply": ([_U64, _U64, C.POINTER(_U64)], C.c_int),
-    "camel_chain_plan": ([_U64, _I64, C.POINTER(_I64), C.c_char_p, C.c_size_t,
+    "camel_chain_plan": ([_U64, _I64, C.POINTER(_I64), C.c_uint32, C.c_char_p, C.c_size_t,
                           C.POINTER(C.c_size_t)], C.c_int),
     "camel_chain_release": ([_U64], C.c_int),
 }
@@ -501,13 +501,13 @@ class Chain:
         _check(load().camel_chain_apply(self.handle, x.handle, C.byref(out)))
         return Tensor(out.value)
 
-    def plan(self, shape) -> list[str]:
+    def plan(self, shape, dtype: int = TC_FLOAT32) -> list[str]:
         dims = (_I64 * max(len(shape), 1))(*shape)
         need = C.c_size_t()
         L = load()
-        _check(L.camel_chain_plan(self.handle, len(shape), dims, None, 0, C.byref(need)))
+        _check(L.camel_chain_plan(self.handle, len(shape), dims, dtype, None, 0, C.byref(need)))
         buf = C.create_string_buffer(need.value)
-        _check(L.camel_chain_plan(self.handle, len(shape), dims, buf, need.value, None))
+        _check(L.camel_chain_plan(self.handle, len(shape), dims, dtype, buf, need.value, None))
         return [line for line in buf.value.decode().split("\n") if line]
 
     def release(self) -> None:

@@ -103,6 +103,13 @@ void *camel_hip_stream(void);
 int camel_hip_malloc(void **ptr, size_t bytes);
 /* Returns a block to the pool (NULL is a no-op). */
 int camel_hip_free(void *ptr);
+/* Releases a block that other streams may still read (a zero-copy DLPack
+ * export whose consumer's deleter ran): it returns to the pool only after a
+ * later device-wide synchronisation, which the library runs at its next pool
+ * miss, camel_hip_device_sync or camel_hip_pool_trim; the call itself never
+ * waits.  No reference counterpart (the reference exports host copies only,
+ * runtime.cpp:1079-1100). */
+int camel_hip_free_shared(void *ptr);
 /* Releases every cached free block to the driver. */
 int camel_hip_pool_trim(void);
 /* Bytes currently handed out / cached, for leak checks. */

@@ -173,10 +173,11 @@ int camel_chain_create(uint64_t *chain);
 int camel_chain_append(uint64_t chain, const char *uri, int64_t n_with, const camel_value *with);
 /* x -> chain: a new tensor handle.  Errors carry the failing layer's text. */
 int camel_chain_apply(uint64_t chain, uint64_t x, uint64_t *result);
-/* The kernel groups apply would run for an input of this shape, one per line
- * (e.g. "conv2d_relu+maxpool2d(2,2) x=nhwc"), NUL-terminated into buf. */
-int camel_chain_plan(uint64_t chain, int64_t rank, const int64_t *shape, char *buf, size_t cap,
-                     size_t *needed);
+/* The kernel groups apply would run for an input of this shape and dtype (a
+ * CAMEL_TC_* code; the fused kernels serve Float32 only), one per line (e.g.
+ * "conv2d_relu+maxpool2d(2,2) x=nchw4"), NUL-terminated into buf. */
+int camel_chain_plan(uint64_t chain, int64_t rank, const int64_t *shape, uint32_t dtype, char *buf,
+                     size_t cap, size_t *needed);
 int camel_chain_release(uint64_t chain);
 
 /* The plugin ABI version the reference's module loader checks before it calls

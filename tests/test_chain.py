@@ -125,3 +125,20 @@ def test_chain_handles():
     assert lib.camel_chain_release(c.handle or 12345) == T.ERR_ARG
     out = T.C.c_uint64()
     assert lib.camel_chain_apply(777, 0, T.C.byref(out)) == T.ERR_ARG
+
+
+def test_plan_follows_the_input_dtype():
+    # The fused conv pair serves Float32 inputs only: for an Int64 input plan()
+    # lists the per-layer groups that apply() runs, and apply() stops at the
+    # first conv with the layer's own error, before any device work.
+    c = cnn_chain()
+    assert c.plan((512, 1, 28, 28), T.TC_INT64)[:2] == [
+        "conv2d_relu y=nchw4", "conv2d_relu+maxpool2d(2,2) x=nchw4"]
+    assert c.plan((512, 1, 28, 28), T.TC_BOOL) == c.plan((512, 1, 28, 28), T.TC_INT64)
+    # Float64 and Int32 are normalised as tensor creation does (runtime.cpp:553-566)
+    assert c.plan((512, 1, 28, 28), T.TC_FLOAT64) == c.plan((512, 1, 28, 28))
+    x = T.Tensor.from_numpy(np.zeros((2, 1, 28, 28), np.int64))
+    with pytest.raises(T.CamelError, match="conv2d requires Float32 tensors"):
+        c(x)
+    with pytest.raises(T.CamelError, match="not a tensor dtype"):
+        c.plan((512, 1, 28, 28), T.TC_VOID)

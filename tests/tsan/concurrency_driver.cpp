@@ -113,7 +113,7 @@ void worker(int id, int iterations) {
                     fail(id, "chain append");
                 char plan[128];
                 size_t need = 0;
-                if (camel_chain_plan(chain, 2, shape, plan, sizeof plan, &need) ||
+                if (camel_chain_plan(chain, 2, shape, CAMEL_TC_FLOAT32, plan, sizeof plan, &need) ||
                     std::strcmp(plan, "dense_relu+softmax\n") != 0)
                     fail(id, "chain plan");
                 if (camel_chain_release(chain)) fail(id, "chain release");
