@@ -1,6 +1,7 @@
 // Runtime part of libcamel_hip.so: device selection, the single stream, the
 // pooled device allocator, boundary copies, events and the creation kernels.
 #include "common.h"
+#include "host_copy.h"
 
 #include <cstdio>
 #include <cstring>
@@ -29,7 +30,22 @@ struct State {
     bool deferred_warned = false;
     size_t in_use = 0;
     size_t cached = 0;
+    // Pinned staging ring of the boundary copies (made at the first large
+    // copy; null if pinned memory could not be had: copies then go direct).
+    char *staging = nullptr;
+    hipEvent_t slot_done[3] = {};
+    bool staging_tried = false;
+    CopyPool *copy_pool = nullptr;
 };
+
+// Staged boundary copies: 3 pinned slots of 8 MiB (measured on MI355X with
+// 64 MiB copies: 44-48 GB/s each way for 3-6 slots of 4-16 MiB and 1-7 copy
+// threads beside the caller; pinned DMA alone 57 GB/s, pageable 17-29 GB/s);
+// copies below 2 MiB go direct (the staging's per-slot waits would dominate
+// them).
+constexpr int STAGING_SLOTS = 3;
+constexpr size_t STAGING_SLOT_BYTES = size_t(8) << 20;
+constexpr size_t STAGING_MIN_BYTES = size_t(2) << 20;
 
 State &state() {
     static State s;
@@ -220,6 +236,93 @@ __global__ void arange_kernel(int64_t *p, int64_t start, int64_t step, int64_t c
 
 } // namespace
 
+namespace {
+
+// The staging ring and its copy threads, made on first use (library mutex
+// held).  False when pinned memory or events could not be had.
+bool staging_ready() {
+    State &s = state();
+    if (s.staging) return true;
+    if (s.staging_tried) return false;
+    s.staging_tried = true;
+    void *p = nullptr;
+    if (hipHostMalloc(&p, STAGING_SLOTS * STAGING_SLOT_BYTES, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    for (int k = 0; k < STAGING_SLOTS; ++k) {
+        if (hipEventCreateWithFlags(&s.slot_done[k], hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            for (int j = 0; j < k; ++j) (void)hipEventDestroy(s.slot_done[j]);
+            (void)hipHostFree(p);
+            return false;
+        }
+    }
+    // three threads beside the caller: four host copies in parallel
+    const unsigned hw = std::thread::hardware_concurrency();
+    s.copy_pool = new CopyPool(hw >= 8 ? 3 : (hw > 1 ? (int)hw - 1 : 0));
+    s.staging = static_cast<char *>(p);
+    return true;
+}
+
+// Host -> device through the pinned slots: slot k is refilled once its
+// previous DMA has completed, while the DMA of the slot before runs.
+int staged_h2d(char *dst, const char *src, size_t bytes) {
+    State &s = state();
+    bool busy[STAGING_SLOTS] = {};
+    int rc = CAMEL_HIP_OK;
+    for_each_chunk(bytes, STAGING_SLOT_BYTES, [&](size_t i, size_t off, size_t m) {
+        if (rc != CAMEL_HIP_OK) return;
+        const int k = (int)(i % STAGING_SLOTS);
+        char *slot = s.staging + k * STAGING_SLOT_BYTES;
+        if (busy[k] && (rc = check_hip(hipEventSynchronize(s.slot_done[k]), "hipEventSynchronize")))
+            return;
+        s.copy_pool->copy(slot, src + off, m);
+        if ((rc = check_hip(hipMemcpyAsync(dst + off, slot, m, hipMemcpyHostToDevice, stream()),
+                            "hipMemcpyAsync(H2D)")))
+            return;
+        rc = check_hip(hipEventRecord(s.slot_done[k], stream()), "hipEventRecord");
+        busy[k] = true;
+    });
+    // every DMA that was enqueued has finished reading its slot before return
+    const int sync = check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+    return rc != CAMEL_HIP_OK ? rc : sync;
+}
+
+// Device -> host: the DMAs of the next slots run while the host copies the
+// slot that has landed out to the destination.
+int staged_d2h(char *dst, const char *src, size_t bytes) {
+    State &s = state();
+    struct Chunk {
+        size_t off, size;
+    };
+    std::vector<Chunk> chunks;
+    for_each_chunk(bytes, STAGING_SLOT_BYTES,
+                   [&](size_t, size_t off, size_t m) { chunks.push_back({off, m}); });
+    auto issue = [&](size_t i) {
+        const int k = (int)(i % STAGING_SLOTS);
+        CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(s.staging + k * STAGING_SLOT_BYTES,
+                                                 src + chunks[i].off, chunks[i].size,
+                                                 hipMemcpyDeviceToHost, stream()),
+                                  "hipMemcpyAsync(D2H)"));
+        return check_hip(hipEventRecord(s.slot_done[k], stream()), "hipEventRecord");
+    };
+    int rc = CAMEL_HIP_OK;
+    for (size_t i = 0; i < chunks.size() && i < (size_t)STAGING_SLOTS && rc == CAMEL_HIP_OK; ++i)
+        rc = issue(i);
+    for (size_t i = 0; i < chunks.size() && rc == CAMEL_HIP_OK; ++i) {
+        const int k = (int)(i % STAGING_SLOTS);
+        rc = check_hip(hipEventSynchronize(s.slot_done[k]), "hipEventSynchronize");
+        if (rc != CAMEL_HIP_OK) break;
+        s.copy_pool->copy(dst + chunks[i].off, s.staging + k * STAGING_SLOT_BYTES, chunks[i].size);
+        if (i + STAGING_SLOTS < chunks.size()) rc = issue(i + STAGING_SLOTS);
+    }
+    const int sync = check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize");
+    return rc != CAMEL_HIP_OK ? rc : sync;
+}
+
+} // namespace
+
 } // namespace camel_hip
 
 using namespace camel_hip;
@@ -367,6 +470,10 @@ int camel_hip_h2d(void *dst, const void *src, size_t bytes) {
     if (!dst || !src) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_h2d: null pointer");
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
+    if (bytes >= STAGING_MIN_BYTES && staging_ready()) {
+        CAMEL_RETURN_IF(staged_h2d(static_cast<char *>(dst), static_cast<const char *>(src), bytes));
+        return ok();
+    }
     CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream()),
                               "hipMemcpyAsync(H2D)"));
     CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));
@@ -378,6 +485,10 @@ int camel_hip_d2h(void *dst, const void *src, size_t bytes) {
     if (!dst || !src) return fail(CAMEL_HIP_ERR_ARG, "camel_hip_d2h: null pointer");
     CAMEL_LOCK();
     CAMEL_INIT_OR_RETURN();
+    if (bytes >= STAGING_MIN_BYTES && staging_ready()) {
+        CAMEL_RETURN_IF(staged_d2h(static_cast<char *>(dst), static_cast<const char *>(src), bytes));
+        return ok();
+    }
     CAMEL_RETURN_IF(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream()),
                               "hipMemcpyAsync(D2H)"));
     CAMEL_RETURN_IF(check_hip(hipStreamSynchronize(stream()), "hipStreamSynchronize"));

@@ -397,3 +397,41 @@ def test_pool_does_not_leak():
     in_use1 = C.c_size_t()
     H.call("camel_hip_pool_stats", C.byref(in_use1), None)
     assert in_use1.value == in_use0.value
+
+
+@pytest.mark.parametrize("nbytes", [(2 << 20) - 1, 2 << 20, (8 << 20) - 1, 8 << 20, (8 << 20) + 1,
+                                    (24 << 20) + 5, 67108864 + 8 * 4096 + 3])
+def test_boundary_copies_through_the_staging_ring(nbytes):
+    # camel_hip_h2d / camel_hip_d2h at and around the staging slots' edges
+    # (copies >= 2 MiB go through 8 MiB pinned slots), from and into host
+    # buffers at every offset mod 8 that the tests reach (the reference's
+    # payload is 8-byte aligned only, runtime.cpp:482-485).  Each direction
+    # is checked against the direct path on its own: the staged upload is
+    # read back in 1 MiB pieces (below the staging threshold), and the staged
+    # download reads a buffer uploaded in 1 MiB pieces.
+    piece = 1 << 20
+    rng = np.random.default_rng(nbytes)
+
+    def direct(name, dev, host_ptr):
+        for o in range(0, nbytes, piece):
+            m = min(piece, nbytes - o)
+            a, b = (C.c_void_p(dev + o), C.c_void_p(host_ptr + o)) if name == "camel_hip_h2d" \
+                else (C.c_void_p(host_ptr + o), C.c_void_p(dev + o))
+            H.call(name, a, b, C.c_size_t(m))
+
+    for off_in, off_out in ((0, 0), (1, 5), (3, 8), (8, 1)):
+        raw = rng.integers(0, 256, size=nbytes + 16, dtype=np.uint8)
+        src = raw.ctypes.data + off_in
+        want = raw[off_in:off_in + nbytes]
+        d = H.DeviceBuffer(nbytes)
+        H.call("camel_hip_h2d", C.c_void_p(d.ptr), C.c_void_p(src), C.c_size_t(nbytes))
+        back = np.full(nbytes + 16, 0xA5, dtype=np.uint8)
+        direct("camel_hip_d2h", d.ptr, back.ctypes.data + off_out)
+        assert np.array_equal(back[off_out:off_out + nbytes], want), "staged upload"
+        e = H.DeviceBuffer(nbytes)
+        direct("camel_hip_h2d", e.ptr, src)
+        back[:] = 0xA5
+        H.call("camel_hip_d2h", C.c_void_p(back.ctypes.data + off_out), C.c_void_p(e.ptr),
+               C.c_size_t(nbytes))
+        assert np.array_equal(back[off_out:off_out + nbytes], want), "staged download"
+        assert np.all(back[:off_out] == 0xA5) and np.all(back[off_out + nbytes:] == 0xA5)
