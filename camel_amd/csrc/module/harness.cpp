@@ -235,6 +235,20 @@ int64_t camel_tensor_live_count(void) { return (int64_t)liveTensorCount(); }
 
 int64_t camel_tensor_release_all(void) { return (int64_t)releaseAll(); }
 
+uint64_t camel_tensor_mark(void) { return registryMark(); }
+
+int camel_tensor_release_since(uint64_t mark, int64_t n_keep, const uint64_t *keep,
+                               int64_t *released) {
+    if (n_keep < 0 || (n_keep > 0 && !keep))
+        return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_release_since: bad arguments");
+    std::vector<const void *> kept;
+    kept.reserve((size_t)n_keep);
+    for (int64_t i = 0; i < n_keep; ++i) kept.push_back(reinterpret_cast<const void *>(keep[i]));
+    const size_t n = releaseSince(mark, kept);
+    if (released) *released = (int64_t)n;
+    return ok();
+}
+
 int camel_tensor_format(uint64_t handle, char *buf, size_t cap, size_t *needed) {
     TensorObject *t = tensorOf(handle);
     if (!t) return fail(CAMEL_TENSOR_ERR_ARG, "camel_tensor_format: not a live tensor");

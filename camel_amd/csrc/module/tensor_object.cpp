@@ -11,6 +11,7 @@
 #include <iostream>
 #include <sstream>
 #include <unordered_map>
+#include <unordered_set>
 
 namespace camel_amd::tensor {
 
@@ -757,6 +758,37 @@ bool isLiveArray(const ArrayObject *a) {
 size_t liveTensorCount() {
     std::lock_guard<std::mutex> lock(registry().mutex);
     return registry().tensors.size();
+}
+
+uint64_t registryMark() {
+    std::lock_guard<std::mutex> lock(registry().mutex);
+    return registry().next - 1;
+}
+
+size_t releaseSince(uint64_t mark, std::span<const void *const> keep) {
+    std::unordered_set<const void *> kept(keep.begin(), keep.end());
+    std::vector<TensorObject *> tensors;
+    std::vector<ArrayObject *> arrays;
+    {
+        std::lock_guard<std::mutex> lock(registry().mutex);
+        auto take = [&](auto &live, auto &out) {
+            for (auto it = live.begin(); it != live.end();) {
+                if (it->second > mark && !kept.count(it->first)) {
+                    out.push_back(it->first);
+                    it = live.erase(it);
+                } else {
+                    ++it;
+                }
+            }
+        };
+        take(registry().tensors, tensors);
+        take(registry().arrays, arrays);
+    }
+    // a view keeps its payload alive through the shared Storage, so the
+    // objects can go in any order
+    for (TensorObject *t : tensors) delete t;
+    for (ArrayObject *a : arrays) delete a;
+    return tensors.size() + arrays.size();
 }
 
 size_t releaseAll() {

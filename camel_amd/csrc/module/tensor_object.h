@@ -180,6 +180,12 @@ bool isLiveArray(const ArrayObject *a);
 size_t liveTensorCount();
 // Releases every registered tensor and array; returns how many objects.
 size_t releaseAll();
+// The registry's serial counter: every object registered later has a larger
+// serial number.
+uint64_t registryMark();
+// Releases every tensor and array registered after `mark` except the objects
+// (tensors or arrays) in `keep`; returns how many objects were released.
+size_t releaseSince(uint64_t mark, std::span<const void *const> keep);
 
 // Cleanup of an operator that throws: while a scope is active on a thread,
 // every tensor and array registered on that thread is recorded in it.  When

@@ -84,6 +84,8 @@ _SIG = {
     "camel_tensor_device_ptr": ([_U64, C.POINTER(_U64)], C.c_int),
     "camel_tensor_release": ([_U64], C.c_int),
     "camel_tensor_release_all": ([], _I64),
+    "camel_tensor_mark": ([], _U64),
+    "camel_tensor_release_since": ([_U64, _I64, C.POINTER(_U64), C.POINTER(_I64)], C.c_int),
     "camel_tensor_live_count": ([], _I64),
     "camel_tensor_format": ([_U64, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)], C.c_int),
     "camel_tensor_equals": ([_U64, _U64, C.POINTER(C.c_int)], C.c_int),
@@ -471,6 +473,21 @@ def live_count() -> int:
 
 def release_all() -> int:
     return int(load().camel_tensor_release_all())
+
+
+def mark() -> int:
+    """A mark for release_since: objects made after it have larger serials."""
+    return int(load().camel_tensor_mark())
+
+
+def release_since(mark_: int, keep=()) -> int:
+    """Releases every tensor / array made after mark_ except those in keep
+    (Tensor objects or raw handles); returns how many were released."""
+    handles = [k.handle if hasattr(k, "handle") else int(k) for k in keep]
+    arr = (_U64 * max(len(handles), 1))(*handles)
+    n = _I64()
+    _check(load().camel_tensor_release_since(mark_, len(handles), arr, C.byref(n)))
+    return int(n.value)
 
 
 class Chain:

@@ -78,6 +78,17 @@ int camel_tensor_device_ptr(uint64_t handle, uint64_t *device_ptr);
 int camel_tensor_release(uint64_t handle);
 /* Releases every tensor and array this layer has made; returns how many. */
 int64_t camel_tensor_release_all(void);
+/* Scoped release for a loop whose iterations make temporaries (e.g. the
+ * train loop of test/run/nn/mnist.cml:44-58, where the reference frees
+ * nothing: no finalizers, include/camel/core/mm/gen.h:224).  camel_tensor_mark
+ * returns a mark; camel_tensor_release_since releases every tensor and array
+ * handle made after that mark except the n_keep handles in keep (e.g. the
+ * updated weights a later iteration reads), and reports how many it released.
+ * Views share their payload, so a kept view keeps it alive.  No reference
+ * counterpart: the reference never releases tensors. */
+uint64_t camel_tensor_mark(void);
+int camel_tensor_release_since(uint64_t mark, int64_t n_keep, const uint64_t *keep,
+                               int64_t *released);
 int64_t camel_tensor_live_count(void);
 /* Writes the reference print form (TensorObject::print) into buf. */
 int camel_tensor_format(uint64_t handle, char *buf, size_t cap, size_t *needed);

@@ -417,3 +417,55 @@ def test_clone_is_a_deep_copy_with_its_own_handle():
     np.testing.assert_array_equal(c.numpy(), x)
     with pytest.raises(T.CamelError):
         T.Tensor(12345).clone()
+
+
+def test_release_since_bounds_a_loop_to_its_live_values():
+    # A train loop (test/run/nn/mnist.cml:44-58) makes temporaries every
+    # iteration; the reference frees none.  With one mark before the loop and
+    # release_since keeping only the new weights at each iteration's end, the
+    # previous weights and every temporary go, and the live count stays flat.
+    T.release_all()
+    w = host(np.arange(12, dtype=np.float32).reshape(3, 4))
+    counts = []
+    m = T.mark()
+    for it in range(4):
+        live0 = T.live_count()
+        tt = T.call("transpose", w)                       # a view of w
+        r = T.call("reshape", tt, [12])                   # another view (and a shape Array)
+        arr = T.Array.from_list([[1.0, 2.0], [3.0, 4.0]])  # array temporaries
+        w_next = T.call("reshape", r, [4, 3]).clone()      # the "updated weights"
+        assert arr.to_list() == [[1.0, 2.0], [3.0, 4.0]]
+        made_tensors = T.live_count() - live0              # tt, r, reshape(r), w_next
+        assert made_tensors == 4
+        released = T.release_since(m, keep=[w_next])
+        # the three tensor temporaries and every array (the nested list, the
+        # shape arguments)
+        assert released >= 3 + 3
+        # w_next stays; the previous weights go too (made after the mark)
+        # except the loop's initial ones
+        assert T.live_count() == (live0 + 1 if it == 0 else live0)
+        with pytest.raises(T.CamelError):
+            tt.numpy()
+        w = w_next
+        counts.append(T.live_count())
+    assert counts[1:] == counts[:-1], counts                # no growth per iteration
+    assert w.shape == (4, 3)
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    want = x
+    for _ in range(4):
+        want = want.T.reshape(4, 3)
+    np.testing.assert_array_equal(w.numpy(), want)
+    # a kept view keeps its payload when its source is released
+    src = host(x)
+    m = T.mark()
+    view = T.call("transpose", src)
+    src.release()
+    assert T.release_since(m, keep=[view]) == 0
+    np.testing.assert_array_equal(view.numpy(), x.T)
+    # objects made before the mark are never touched
+    before = T.live_count()
+    assert T.release_since(T.mark()) == 0 and T.live_count() == before
+    with pytest.raises(T.CamelError, match="bad arguments"):
+        load = T.load()
+        import ctypes as C
+        T._check(load.camel_tensor_release_since(0, -1, None, None))
