@@ -1343,23 +1343,25 @@ int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, c
 // Skinny GEMM (M <= 32, e.g. M = 16, N = K = 4096): B is read once from HBM
 // and dominates the traffic, so the kernel is a streaming pass over B.
 //   * a work-group owns 64 columns x SK_CHUNK * CH k; its 8 waves take
-//     interleaved chunks (wave w, chunk c: rows kb0 + (8 c + w) * 32 .. +31),
+//     interleaved chunks (wave w, chunk c: rows kb0 + (8 c + w) * 16 .. +15),
 //     so at any time the work-group reads one contiguous block of rows;
-//   * within a chunk lane l takes rows base + 8 (l / 16) + s (s = 0..7) and
+//   * within a chunk lane l takes rows base + 4 (l / 16) + s (s = 0..3) and
 //     one 16-byte piece of each, columns n0 + 4 (l % 16) .. +3: one load
 //     instruction covers 4 rows x 256 contiguous bytes;
 //   * v_mfma_f32_16x16x4_f32 takes A[i][k] from lane i + 16 k and B[k][j]
 //     from lane j + 16 k; the 4 floats of a lane's piece feed 4 MFMAs whose
 //     column j stands for column n0 + 4 j + c (c = 0..3), so no shuffle is
 //     needed; the accumulator of MFMA c holds rows 4 (l / 16) + v at column
-//     n0 + 4 (l % 16) + c.  Lane l's 8 k of a chunk are contiguous, so its A
-//     values are two 16-byte loads (A is small and stays in L2);
+//     n0 + 4 (l % 16) + c.  Lane l's 4 k of a chunk are contiguous, so its A
+//     values are one 16-byte load (A is small and stays in L2);
 //   * B is read with nontemporal loads (it is read once; they measured 7%
-//     faster than cached ones), a chunk's 8 loads issued together and
+//     faster than cached ones), a chunk's 4 loads issued together and
 //     multiplied once they land -- a register double buffer that kept the
 //     next chunk in flight measured 2% slower (the 8 waves of a CU already
 //     overlap one another's loads); scheduling barriers keep the compiler
-//     from interleaving a chunk's loads with its MFMAs;
+//     from interleaving a chunk's loads with its MFMAs.  Chunks of 4 rows
+//     per lane rather than 8 halve the last chunk's MFMAs, which no load
+//     overlaps (16 x 4096 x 4096: 16.07 -> 15.31 us per call);
 //   * the 8 waves' sums meet in LDS in wave order; thread x then owns row
 //     x / 16 and 4 consecutive columns, so the results (or the partials of
 //     work-groups along K, [ks][M][N], which skinny_reduce_kernel sums in ks
@@ -1373,7 +1375,7 @@ int launch_thin(const float *A, const float *B, float *C, int M, int N, int K, c
 // the guard-free path).
 constexpr int SK_WAVES = 8;
 constexpr int SK_COLS = 64;
-constexpr int SK_STEPS = 8;                          // 4-row MFMA steps per chunk and wave
+constexpr int SK_STEPS = 4;                          // 4-row MFMA steps per chunk and wave
 constexpr int SK_CHUNK = SK_WAVES * 4 * SK_STEPS;    // k rows per chunk of the work-group
 constexpr int SK_MAX_KGROUPS = 65535;                // grid.y limit
 
@@ -1500,16 +1502,30 @@ __global__ __launch_bounds__(SK_WAVES * 64) void sgemm_skinny_kernel(
 // Sums the skinny kernel's k partials in ks order, then bias and relu; one
 // thread per 4 consecutive outputs of a row (N % 4 == 0).  Small work-groups
 // (SK_REDUCE_THREADS) spread the few outputs over many CUs; the partials are
-// read once, with nontemporal loads.
+// read once, with nontemporal loads.  With `strips` > 0 (N a multiple of
+// SK_COLS), work-group b takes 4 rows of strip b % strips: the skinny
+// kernel's work-groups of that strip (block ids strip + strips * ks) ran on
+// the same XCD when strips % 8 == 0, so the partials are read from that
+// XCD's L2 (16 x 4096 x 4096: 15.30 -> 15.03 us per call); otherwise one
+// thread per float4 in row-major order.
 constexpr int SK_REDUCE_THREADS = 64;
+static_assert(SK_REDUCE_THREADS == 4 * SK_COLS / 4, "a strip-mapped work-group is 4 rows of a strip");
 
 __global__ __launch_bounds__(SK_REDUCE_THREADS) void skinny_reduce_kernel(
     const float4 *__restrict__ partial, float4 *__restrict__ C, int M, int N, int nks,
-    const float *__restrict__ bias, int flags) {
+    const float *__restrict__ bias, int flags, int strips) {
     typedef float floatx4 __attribute__((ext_vector_type(4)));
     const size_t total4 = (size_t)M * N / 4;
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= total4) return;
+    size_t idx;
+    if (strips > 0) {
+        const int strip = blockIdx.x % strips, rows4 = blockIdx.x / strips;
+        const int row = 4 * rows4 + threadIdx.x / (SK_COLS / 4);
+        if (row >= M) return;
+        idx = ((size_t)row * N + (size_t)strip * SK_COLS) / 4 + threadIdx.x % (SK_COLS / 4);
+    } else {
+        idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (idx >= total4) return;
+    }
     const floatx4 *p4 = reinterpret_cast<const floatx4 *>(partial);
     // k groups added in order; their loads go out up to 8 at a time
     const floatx4 y0 = __builtin_nontemporal_load(p4 + idx);
@@ -1962,7 +1978,7 @@ SkinnyPlan plan_skinny(int64_t N, int64_t K) {
     // CU (fewer, longer streams measured faster than more, shorter ones).
     const int cus = std::max(1, device_cu_count());
     int ch = 1;
-    for (int c : {4, 2}) {
+    for (int c : {8, 4, 2}) {
         if (strips * ((K + SK_CHUNK * c - 1) / (SK_CHUNK * c)) >= cus) {
             ch = c;
             break;
@@ -1991,17 +2007,22 @@ int launch_skinny(const float *A, const float *B, float *C, int M, int N, int K,
         CAMEL_RETURN_IF(check_launch("sgemm_skinny_kernel"));
         if (nks == 1) return CAMEL_HIP_OK;
         const int64_t total4 = (int64_t)M * N / 4;
-        hipLaunchKernelGGL(skinny_reduce_kernel,
-                           dim3((unsigned)((total4 + SK_REDUCE_THREADS - 1) / SK_REDUCE_THREADS)),
-                           dim3(SK_REDUCE_THREADS), 0, stream(), reinterpret_cast<const float4 *>(partial),
-                           reinterpret_cast<float4 *>(C), M, N, nks, bias, flags);
+        const int by_strip = N % SK_COLS == 0 ? strips : 0;
+        const unsigned blocks =
+            by_strip ? (unsigned)(by_strip * ((M + 3) / 4))
+                     : (unsigned)((total4 + SK_REDUCE_THREADS - 1) / SK_REDUCE_THREADS);
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3(blocks), dim3(SK_REDUCE_THREADS), 0, stream(),
+                           reinterpret_cast<const float4 *>(partial), reinterpret_cast<float4 *>(C),
+                           M, N, nks, bias, flags, by_strip);
         return check_launch("skinny_reduce_kernel");
     };
     if (mt == 1) {
+        if (ch == 8) return go(sgemm_skinny_kernel<1, 8>, 8);
         if (ch == 4) return go(sgemm_skinny_kernel<1, 4>, 4);
         if (ch == 2) return go(sgemm_skinny_kernel<1, 2>, 2);
         return go(sgemm_skinny_kernel<1, 1>, 1);
     }
+    if (ch == 8) return go(sgemm_skinny_kernel<2, 8>, 8);
     if (ch == 4) return go(sgemm_skinny_kernel<2, 4>, 4);
     if (ch == 2) return go(sgemm_skinny_kernel<2, 2>, 2);
     return go(sgemm_skinny_kernel<2, 1>, 1);
