@@ -77,3 +77,36 @@ def test_more_than_one_gpu_is_refused(argv, env):
     assert out.returncode == 2
     assert "one GPU only" in out.stderr
     assert out.stdout == ""
+
+
+CLINE = re.compile(r"^(\w+): ([\d.]+)\s+([\d.]+) ([\d.]+)\s+([\d.]+)\s+(.*)$")
+
+
+def test_mfma_counter_table_parses_and_carries_provenance():
+    rows = {}
+    with open(bench.COUNTER_FILE) as f:
+        for line in f:
+            if line.startswith("#") or not line.strip():
+                continue
+            m = CLINE.match(line.rstrip("\n"))
+            assert m, f"malformed counter line: {line!r}"
+            rows[m.group(1)] = m
+    # every MFMA-bound key bench.py asks for
+    for key in ("sgemm_4096", "sgemm_2048", "sgemm_1024", "sgemm_8192", "mlp", "cnn", "conv2d"):
+        assert key in rows, key
+    for key, m in rows.items():
+        busy, issued, algo, lds = (float(m.group(i)) for i in (2, 3, 4, 5))
+        assert 0.0 < busy <= 1.0 and 0.0 <= lds < 1.0, key
+        # the MFMA work issued is the algorithmic work up to padding, or less
+        # where layers run outside the MFMAs (the CNN's conv1 and classifier)
+        assert 0.9 * algo <= issued <= 1.1 * algo, key
+        tags = dict(f.split("=", 1) for f in m.group(6).split())
+        assert re.fullmatch(r"[0-9a-f]{12}", tags["commit"]), key
+        assert all(tags["kernels"].split(";")), key
+    busy, src = bench._counter_entry("sgemm_4096")
+    assert busy == float(rows["sgemm_4096"].group(2))
+    assert src["counters"] == "SQ_VALU_MFMA_BUSY_CYCLES, SQ_BUSY_CU_CYCLES"
+    r = bench.roofline_mfma(137.4e9, 1.0, "sgemm_4096")
+    assert r["mfma_busy"] == busy and r["mfma_busy_source"]["kernels"] == src["kernels"]
+    # bandwidth rows carry no MFMA figure
+    assert "mfma_busy" not in bench.roofline_hbm(4e9, 1.0, "eltwise_relu")

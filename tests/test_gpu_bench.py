@@ -39,6 +39,7 @@ def test_headline_line_keeps_the_contract():
     assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s" and r["peak"] == 157.3
     assert 0 < r["frac"] < 1 and abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
     assert r["traffic"] > 0 and r["traffic_source"]["kernels"]
+    assert 0 < r["mfma_busy"] <= 1 and r["mfma_busy_source"]["kernels"]
     c = d["cpu_baseline"]
     assert c["value"] > 0 and c["cores"] == 1 and c["kind"] == "port" and c["sample"]
 
@@ -47,3 +48,5 @@ def test_single_workload_mode():
     d = _run("--workload", "skinny", "--steps", "5", "--warmup", "2")
     assert d["workload"] == "skinny"
     assert d["ms"] > 0 and d["bytes"] == 4.0 * (16 * 4096 + 4096 * 4096 + 16 * 4096)
+    d = _run("--workload", "gemm1024", "--steps", "5", "--warmup", "2")
+    assert d["workload"] == "gemm1024" and d["ms"] > 0 and d["value"] > 0
