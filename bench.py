@@ -224,8 +224,9 @@ def wl_skinny(steps, warmup):
 
 def wl_mlp(steps, warmup, fused=True):
     """MLP forward: dense 784->1024->1024->10 (+relu) then row softmax, batch 1024.
-    fused: the classifier layer and the softmax run as one kernel
-    (camel_hip_dense_softmax); otherwise GEMM then the softmax kernel."""
+    fused: the calls the operator layer's chain makes for it (its plan is
+    dense_relu, then dense_relu+dense+softmax as camel_hip_dense_head);
+    otherwise one call per layer and the softmax kernel."""
     B = 1024
     dims = [784, 1024, 1024, 10]
     x = D.uniform(D.SEED_MLP, (B, dims[0]), 0.0, 1.0)
@@ -238,17 +239,21 @@ def wl_mlp(steps, warmup, fused=True):
     acts = [H.DeviceBuffer(B * d * 4) for d in dims[1:]]
     dp = H.DeviceBuffer(B * 10 * 4)
 
+    relu_bias = H.EPI_BIAS | H.EPI_RELU
+
     def step():
+        if fused:
+            sgemm_call(dx, dws[0], acts[0], B, dims[1], dims[0], dbs[0], relu_bias)()
+            H.call("camel_hip_dense_head", P(acts[0].ptr), P(dws[1].ptr), P(dbs[1].ptr),
+                   P(dws[2].ptr), P(dbs[2].ptr), P(dp.ptr), B, dims[1], dims[2], dims[3],
+                   relu_bias, H.EPI_BIAS, 1)
+            return
         src = dx
-        for i in range(2 if fused else 3):
+        for i in range(3):
             flags = H.EPI_BIAS | (H.EPI_RELU if i < 2 else 0)
             sgemm_call(src, dws[i], acts[i], B, dims[i + 1], dims[i], dbs[i], flags)()
             src = acts[i]
-        if fused:
-            H.call("camel_hip_dense_softmax", P(acts[1].ptr), P(dws[2].ptr), P(dbs[2].ptr), P(dp.ptr),
-                   B, 10, dims[2], H.EPI_BIAS)
-        else:
-            H.call("camel_hip_softmax_rows", P(acts[2].ptr), P(dp.ptr), B, 10)
+        H.call("camel_hip_softmax_rows", P(acts[2].ptr), P(dp.ptr), B, 10)
 
     ms, wall = _time_loop(step, steps, warmup)
     flop = sum(2.0 * B * dims[i] * dims[i + 1] for i in range(3))

@@ -139,7 +139,21 @@ struct GemmArgs {
     // LOAD_PLANES: distance between channel planes (H * W); pxs = 1 and
     // cqs = 4 * H * W
     int chs;
+    // Classifier head (64 x 64 tiles, row-major operands): instead of C, each
+    // tile stores its columns' share of the next layer's products,
+    // head_partial[tn][m][n] = sum_j C[m][64 tn + j] * head_w[64 tn + j][n]
+    // (j ascending) for n < head_n2 <= 16, where C is the finished tile (bias,
+    // relu); null for an ordinary GEMM.
+    const float *head_w;
+    float *head_partial;
+    int head_n2;
 };
+
+// Tiles whose epilogue can run the classifier head (GemmArgs::head_w).
+template <class T, int AMODE, int BMODE>
+constexpr bool head_tile = T::BM == 64 && T::BN == 64 && T::WK == 2 && T::FM == 1 && T::FN == 1 &&
+                           AMODE == LOAD_VEC && BMODE == LOAD_VEC;
+constexpr int HEAD_MAX_N2 = 16;
 
 // (pixel, k-quad) of B item q of a stage: NHWC-style loaders put a pixel's
 // k-quads on consecutive lanes (one 16-byte load each); the plane loaders put
@@ -227,6 +241,22 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     block_pos(local, split);
     tile_of(g.tile_begin + local, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * T::BM, n0 = g.n_begin + tn * T::BN;
+    // Classifier head: this tile's rows of the next layer's weights, loaded
+    // before the K loop so that their latency hides behind it.
+    constexpr bool HEAD = head_tile<T, AMODE, BMODE>;
+    const bool head = HEAD && g.head_w != nullptr;
+    float head_wr[2] = {0.f, 0.f};
+    if constexpr (HEAD) {
+        static_assert(T::BN * HEAD_MAX_N2 <= 2 * T::THREADS, "two head weights per thread");
+        if (head) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int e = (int)threadIdx.x + u * T::THREADS;
+                if (e < T::BN * g.head_n2)
+                    head_wr[u] = g.head_w[(size_t)(n0 + e / g.head_n2) * g.head_n2 + e % g.head_n2];
+            }
+        }
+    }
     // K is consumed in whole stages: when BK does not divide K, the ragged
     // part is the first stage of split 0, which starts kpad below k = 0 and
     // is loaded with guards (zeros below 0); every later stage is a whole BK
@@ -791,8 +821,8 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                                                              acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
         }
         __syncthreads();
-        if (wk > 0) return;
-        for (int grp = 1; grp < T::WK; ++grp) {
+        if (wk > 0 && !head) return;
+        for (int grp = 1; grp < (wk == 0 ? T::WK : 1); ++grp) {
 #pragma unroll
             for (int i = 0; i < T::FM; ++i)
 #pragma unroll
@@ -805,6 +835,50 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                         acc[i][j][4 * q + 2] += v.z;
                         acc[i][j][4 * q + 3] += v.w;
                     }
+        }
+    }
+
+    if constexpr (HEAD) {
+        if (head) {
+            // Group 0 leaves the finished tile (bias, relu: the values the
+            // store below would write) in LDS past the k-group sums; every
+            // thread then forms (row, n) sums over the tile's 64 columns.
+            constexpr int HS = T::BN + 1; // padded row of the tile
+            static_assert(T::BM * T::BN + T::BM * HS + T::BN * HEAD_MAX_N2 <= 2 * T::STAGE,
+                          "head tile and weights fit beside the k-group sums");
+            float *ht = smem + T::BM * T::BN;
+            float *hw = ht + T::BM * HS;
+            const int n2 = g.head_n2;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int e = (int)threadIdx.x + u * T::THREADS;
+                if (e < T::BN * n2) hw[(e / n2) * HEAD_MAX_N2 + e % n2] = head_wr[u];
+            }
+            if (wk == 0) {
+                const bool hb = (g.flags & CAMEL_EPI_BIAS) != 0, hr = (g.flags & CAMEL_EPI_RELU) != 0;
+                const int col = wn * T::WTN + r32;
+                const float bc = hb ? g.bias[n0 + col] : 0.f;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int row = wm * T::WTM + 8 * (v >> 2) + 4 * half + (v & 3);
+                    float x = acc[0][0][v];
+                    if (hb) x = x + bc;
+                    if (hr) x = relu_idiom(x);
+                    ht[row * HS + col] = x;
+                }
+            }
+            __syncthreads();
+            // (Splitting each sum over a lane quad, 16 columns a lane, measured
+            // slower: MLP forward 47.1 -> 49.2 us.)
+            for (int o = (int)threadIdx.x; o < T::BM * n2; o += T::THREADS) {
+                const int row = o / n2, n = o - row * n2;
+                float s = 0.f;
+#pragma unroll 16
+                for (int j = 0; j < T::BN; ++j)
+                    s = __builtin_fmaf(ht[row * HS + j], hw[j * HEAD_MAX_N2 + n], s);
+                g.head_partial[((size_t)tn * g.M + m0 + row) * n2 + n] = s;
+            }
+            return;
         }
     }
 
@@ -1290,6 +1364,35 @@ __global__ __launch_bounds__(1024) void sgemm_thin_rows_kernel(const ASrc src,
         }
         __syncthreads(); // quarter[] is rewritten by the next group
     }
+}
+
+// Finishes a classifier head run in a GEMM epilogue (GemmArgs::head_w): row
+// m's N2 outputs are the tiles' partial sums added in tile order, then the
+// second layer's bias and relu (and the row softmax), one wave per row, lane
+// n holding column n -- the layout softmax_row_lanes takes.
+template <bool SOFTMAX>
+__global__ __launch_bounds__(256) void head_finish_kernel(const float *__restrict__ partial,
+                                                          int tiles_n, int M, int N2,
+                                                          const float *__restrict__ bias, int flags,
+                                                          float *__restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return; // whole waves
+    float out = 0.f;
+    if (lane < N2) {
+        const float *p = partial + (size_t)m * N2 + lane;
+        const size_t tile_stride = (size_t)M * N2;
+        float v[HEAD_MAX_N2];
+#pragma unroll
+        for (int t = 0; t < HEAD_MAX_N2; ++t) v[t] = t < tiles_n ? p[t * tile_stride] : 0.f;
+#pragma unroll
+        for (int t = 0; t < HEAD_MAX_N2; ++t)
+            if (t < tiles_n) out = out + v[t];
+        if (flags & CAMEL_EPI_BIAS) out = out + bias[lane];
+        if (flags & CAMEL_EPI_RELU) out = relu_idiom(out);
+    }
+    if constexpr (SOFTMAX) out = softmax_row_lanes(lane < N2 ? out : -INFINITY);
+    if (lane < N2) y[(size_t)m * N2 + lane] = out;
 }
 
 // True when the thin kernel serves C[M, N] = A[M, K] B[K, N].
@@ -3067,6 +3170,35 @@ int camel_hip_dense_head(const float *x, const float *w1, const float *b1, const
     int splits = 1, bk = 0;
     if (N2 <= 16 && thin_eligible(M, N2, N1) && !thin_eligible(M, N1, K1) && M > 32)
         choose(M, N1, K1, device_cu_count(), cfg, splits, bk);
+    const bool avec = (K1 % 4 == 0) && ((uintptr_t)x % 16 == 0);
+    const bool bvec = (N1 % 4 == 0) && ((uintptr_t)w1 % 16 == 0);
+    if (cfg == Cfg::Small && splits <= 1 && avec && bvec && M % TileSmall::BM == 0 &&
+        N1 % TileSmall::BN == 0 && N1 <= (int64_t)HEAD_MAX_N2 * TileSmall::BN &&
+        N2 <= HEAD_MAX_N2 && M <= INT32_MAX / HEAD_MAX_N2) {
+        // Layer 1 runs unsplit on 64 x 64 tiles (e.g. the MLP's 1024 x 1024
+        // -> 1024): each tile's epilogue multiplies its finished 64 columns
+        // by their 64 rows of w2, and head_finish_kernel adds the tiles' sums
+        // in tile order -- layer 1's output never reaches HBM and the thin
+        // kernel's staging of w2 is not needed.
+        const int tiles_m = (int)(M / TileSmall::BM), tiles_n = (int)(N1 / TileSmall::BN);
+        Scratch part;
+        CAMEL_RETURN_IF(part.alloc((size_t)tiles_n * M * N2 * sizeof(float)));
+        GemmArgs g = sgemm_args(x, w1, nullptr, M, N1, K1, b1, flags1);
+        g.head_w = w2;
+        g.head_partial = part.f();
+        g.head_n2 = (int)N2;
+        CAMEL_RETURN_IF((launch_range<TileSmall, LOAD_VEC, LOAD_VEC>(g, 0, tiles_m * tiles_n, 1,
+                                                                      "sgemm_kernel")));
+        const unsigned blocks = (unsigned)((M + 3) / 4);
+        if (softmax)
+            hipLaunchKernelGGL(head_finish_kernel<true>, dim3(blocks), dim3(256), 0, stream(), part.f(),
+                               tiles_n, (int)M, (int)N2, b2, flags2, y);
+        else
+            hipLaunchKernelGGL(head_finish_kernel<false>, dim3(blocks), dim3(256), 0, stream(),
+                               part.f(), tiles_n, (int)M, (int)N2, b2, flags2, y);
+        CAMEL_RETURN_IF(check_launch("head_finish_kernel"));
+        return ok();
+    }
     if (cfg == Cfg::Skinny || splits <= 1) {
         Scratch h;
         CAMEL_RETURN_IF(h.alloc((size_t)(M * N1) * sizeof(float)));
@@ -3086,8 +3218,6 @@ int camel_hip_dense_head(const float *x, const float *w1, const float *b1, const
     g.ldb = (int)N1;
     g.ldc = (int)N1;
     g.flags = flags1;
-    const bool avec = (K1 % 4 == 0) && ((uintptr_t)x % 16 == 0);
-    const bool bvec = (N1 % 4 == 0) && ((uintptr_t)w1 % 16 == 0);
     SplitPartialsA src{};
     switch (cfg) {
     case Cfg::Big:

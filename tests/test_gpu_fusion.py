@@ -28,6 +28,7 @@ from camel_amd import _hip as H
 from camel_amd import datagen as D
 from oracle import ffi as O
 from tests import hipkit as K
+from tests.test_gpu_exact import ints
 
 pytestmark = pytest.mark.gpu
 P = C.c_void_p
@@ -135,7 +136,7 @@ def _head_in_two_calls(x, w1, b1, w2, b2, flags1, flags2, softmax):
     (512, 9216, 128, 10, H.EPI_BIAS | H.EPI_RELU, False),
     (300, 2000, 200, 16, H.EPI_BIAS, True),             # ragged tiles, N2 = 16
     (130, 700, 72, 5, 0, True),                         # 32x32 tiles with K splits
-    (1024, 1024, 1024, 10, H.EPI_BIAS, True),           # the MLP's head: no split, two calls
+    (1000, 1024, 1024, 10, H.EPI_BIAS, True),           # unsplit, M % 64 != 0: two calls
     (257, 300, 24, 9, H.EPI_BIAS, True),                # layer 1 on the thin-N kernel, two calls
 ])
 def test_dense_head_equals_two_calls(M, K1, N1, N2, flags2, softmax):
@@ -152,6 +153,50 @@ def test_dense_head_equals_two_calls(M, K1, N1, N2, flags2, softmax):
     rows = slice(0, 8)
     ok, worst = K.gemm_tol_ok(h[rows], O.dense(x[rows], w1, b1, True), x[rows], w1)
     assert ok, f"layer 1 worst error / bound = {worst}"
+
+
+HEAD_EPILOGUE_SHAPES = [
+    # layer 1 unsplit on 64 x 64 tiles that fill the chip: the head runs in
+    # its epilogue and head_finish_kernel adds the 64-column shares
+    (1024, 1024, 1024, 10),   # the benchmark MLP's head
+    (2048, 512, 512, 16),     # N2 = 16, 8 column tiles
+    (4096, 300, 256, 7),      # K % 64 != 0 (ragged first stage), 4 column tiles
+]
+
+
+@pytest.mark.parametrize("M,K1,N1,N2", HEAD_EPILOGUE_SHAPES)
+def test_dense_head_in_the_gemm_epilogue(M, K1, N1, N2):
+    # Small integers: the logits are exact whatever the order, so they equal
+    # the two calls bit for bit.
+    xi = ints(0x5500 + M, (M, K1), 0, 2)
+    w1i, b1i = ints(0x5501, (K1, N1), -1, 1), ints(0x5502, (N1,), -1, 1)
+    w2i, b2i = ints(0x5503, (N1, N2), -1, 1), ints(0x5504, (N2,), -2, 2)
+    e1 = H.EPI_BIAS | H.EPI_RELU
+    for flags2 in (H.EPI_BIAS, H.EPI_BIAS | H.EPI_RELU):
+        got = _dense_head(xi, w1i, b1i, w2i, b2i, e1, flags2, False)
+        _, ref = _head_in_two_calls(xi, w1i, b1i, w2i, b2i, e1, flags2, False)
+        np.testing.assert_array_equal(got, ref)
+    # Real values: the tiles' shares add in another order than the thin
+    # kernel's, so the logits match the two calls within the GEMM bound of
+    # layer 2, and the fused softmax is the softmax of the fused logits
+    # within the softmax bar.
+    x = D.uniform(0x5600 + M, (M, K1), 0.0, 1.0)
+    w1 = D.normal(0x5601, (K1, N1), std=float(np.sqrt(2.0 / K1)))
+    b1 = D.uniform(0x5602, (N1,), -0.1, 0.1)
+    w2 = D.normal(0x5603, (N1, N2), std=float(np.sqrt(2.0 / N1)))
+    b2 = D.uniform(0x5604, (N2,), -0.1, 0.1)
+    logits = _dense_head(x, w1, b1, w2, b2, e1, H.EPI_BIAS, False)
+    h, ref = _head_in_two_calls(x, w1, b1, w2, b2, e1, H.EPI_BIAS, False)
+    ok, worst = K.gemm_tol_ok(logits, ref, h, w2)
+    assert ok, f"logits worst error / bound = {worst}"
+    p = _dense_head(x, w1, b1, w2, b2, e1, H.EPI_BIAS, True)
+    q = O.softmax_rows(logits)
+    assert np.max(np.abs(p.astype(np.float64) - q) / np.maximum(q, 1e-30)) <= 1e-6
+    # and against the oracle's layers on a few rows
+    rows = slice(M - 4, M)
+    hr = O.dense(x[rows], w1, b1, True)
+    ok, worst = K.gemm_tol_ok(logits[rows], O.dense(hr, w2, b2, False), hr, w2)
+    assert ok, f"oracle logits worst error / bound = {worst}"
 
 
 def test_dense_head_argument_errors():
