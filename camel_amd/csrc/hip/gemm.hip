@@ -2208,6 +2208,7 @@ int launch_range(GemmArgs g, int tile_begin, int ntiles, int splits, const char 
 template <class T>
 using BandTile = Tile<64, (T::BK >= 32 ? 32 : 64), T::BK, 2, (T::BK >= 32 ? 1 : 2),
                       (T::BK >= 32 ? 2 : 1)>;
+using BandTile64 = Tile<64, 32, 64, 2, 1, 2>;
 
 // Schedules all tiles.  `splits` > 1 splits every tile (small problems).
 // Otherwise whole rounds of resident work-groups run as whole tiles, and the
@@ -2266,9 +2267,20 @@ template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, co
     const GemmSchedule s = schedule_gemm<T, AMODE, BMODE>(g, splits);
     CAMEL_RETURN_IF((launch_range<T, AMODE, BMODE>(g, 0, s.head, s.head_splits, name)));
     if (s.band) {
-        using TB = BandTile<T>;
         GemmArgs band = g;
         band.n_begin = s.band_n;
+        if constexpr (T::BK == 32 && is_nhwc<BMODE>) {
+            // stages of 64 channels where the channels allow (a stage stays
+            // within one (kh, kw)): half the stages of the latency-bound
+            // small tiles (config-4 conv: 268.9 -> 266.2 us per call)
+            if (g.Cin % 64 == 0) {
+                using TB = BandTile64;
+                const int band_tiles = (int)((int64_t)((g.M + TB::BM - 1) / TB::BM) *
+                                             ((g.N - band.n_begin + TB::BN - 1) / TB::BN));
+                return launch_range<TB, AMODE, BMODE>(band, 0, band_tiles, 1, name);
+            }
+        }
+        using TB = BandTile<T>;
         const int band_tiles =
             (int)((int64_t)((g.M + TB::BM - 1) / TB::BM) * ((g.N - band.n_begin + TB::BN - 1) / TB::BN));
         return launch_range<TB, AMODE, BMODE>(band, 0, band_tiles, 1, name);
