@@ -2415,7 +2415,8 @@ void choose(int64_t M, int64_t N, int64_t K, int cus, Cfg &cfg, int &splits, int
 //     64 output channels; 4 waves as 2 (channels) x 2 (column halves), each
 //     wave 32 channels x CP_NBW blocks of 32 columns;
 //   * columns in pool order, 4 per window ((0,0), (0,1), (1,0), (1,1)), so a
-//     window is one DPP quad and the epilogue takes its max in registers;
+//     window is one DPP quad and the epilogue takes its max in registers,
+//     and 16 consecutive columns a 2 x 2 block of windows (cp_window);
 //   * conv1 is the direct kernel's FMA chain (k = (kh, kw) ascending, then
 //     bias and x * (x > 0)), so the patch holds exactly the values the conv1
 //     kernel stores;
@@ -2434,11 +2435,15 @@ constexpr int CP_R1 = 2 * CP_BR + 2;      // conv1 rows a band reads (10)
 constexpr int CP_IR = CP_R1 + 2;          // input rows a band reads (12)
 // The patch is stored by channel quads, [C1/4][CP_R1][CP_RS][4]: a lane reads
 // the 4 channels of one pixel that 4 consecutive MFMAs take with one 16-byte
-// read, and with a row pitch of CP_RS = 28 (= 4 mod 8) pixels, the 8 lanes a
-// 16-byte read serves at a time (2 windows: 2 x 4 pixels over 2 or 4 rows)
-// fall on 8 distinct bank groups.
+// read.  A 16-byte LDS read serves 16 lanes per clock, conflict-free when
+// their chunks are distinct mod 16 (64 banks x 4 bytes); those 16 lanes read
+// a 2 x 2 block of windows, pixels (2 py + r, 2 px + c) for r, c in 0..3, and
+// with a row pitch of CP_RS = 28 pixels (28 r = 0, 12, 8, 4 mod 16) the 16
+// chunks are distinct.  (4 windows of one row, 2 rows x 8 pixels, collided
+// 2-way on 4 of the chunks at this pitch; a pitch of 40 clears those too but
+// ran the CNN forward 1.7% slower; the 2 x 2 blocks ran it 0.4% faster.)
 constexpr int CP_RS = 28;
-static_assert(CP_RS >= CP_OW1 && CP_RS % 8 == 4, "conflict-free patch row pitch");
+static_assert(CP_RS >= CP_OW1 && CP_RS % 16 == 12, "conflict-free patch row pitch");
 // One channel quad of the patch: 1120 floats, padded to 1124 (= 4 mod 32) so
 // that the conv1 phase's 32 lanes, one channel each, store one pixel to 32
 // distinct banks.
@@ -2446,6 +2451,15 @@ constexpr int CP_QPLANE = CP_R1 * CP_RS * 4 + 4;
 constexpr int CP_COLS = CP_BR * CP_PW * 4; // GEMM columns of a band (192)
 constexpr int CP_NBW = CP_COLS / 32 / 2;  // 32-column blocks per wave (3)
 static_assert(CP_COLS % 64 == 0, "a band is whole 32-column blocks for both column halves");
+
+// The pool window (row py of the band, column px) of GEMM column col: 4
+// columns per window, and 16 consecutive columns a 2 x 2 block of windows.
+__device__ __forceinline__ void cp_window(int col, int &py, int &px) {
+    static_assert(CP_BR % 2 == 0 && CP_PW % 2 == 0, "windows in 2 x 2 blocks");
+    const int g = col >> 4, w4 = (col >> 2) & 3;
+    py = 2 * (g / (CP_PW / 2)) + (w4 >> 1);
+    px = 2 * (g % (CP_PW / 2)) + (w4 & 1);
+}
 
 __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
     const float *__restrict__ x, const float *__restrict__ w1, const float *__restrict__ b1,
@@ -2513,9 +2527,9 @@ __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
     int base[CP_NBW];
 #pragma unroll
     for (int b = 0; b < CP_NBW; ++b) {
-        const int col = 32 * (CP_NBW * wn + b) + r32;
-        const int win = col >> 2, d = col & 3;
-        const int py = win / CP_PW, px = win - py * CP_PW;
+        const int col = 32 * (CP_NBW * wn + b) + r32, d = col & 3;
+        int py, px;
+        cp_window(col, py, px);
         base[b] = half * CP_QPLANE + ((2 * py + (d >> 1)) * CP_RS + 2 * px + (d & 1)) * 4;
     }
     floatx16 acc[CP_NBW];
@@ -2588,8 +2602,9 @@ __global__ __launch_bounds__(256, 2) void conv_pair_pool_kernel(
 #pragma unroll
     for (int b = 0; b < CP_NBW; ++b) {
         const int col = 32 * (CP_NBW * wn + b) + r32;
-        const int win = col >> 2;
-        const int py = band * CP_BR + win / CP_PW, px = win % CP_PW;
+        int py, px;
+        cp_window(col, py, px);
+        py += band * CP_BR;
         float *out = y + ((size_t)n * Co2 + m0 + 32 * wm) * PH * CP_PW + (size_t)py * CP_PW + px;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
