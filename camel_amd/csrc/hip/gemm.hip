@@ -57,9 +57,18 @@ constexpr int GROUP_M = 4;
 // At [K, M] row-major (A[m][k] = At[k][m]): like B, k rows with the tile's
 // m contiguous, transposed 4x4 in registers before the LDS store, so
 // transpose(X) @ E needs no copy of X (16-byte loads need M % 4 == 0).
+// LOAD_DMA (A and B together, row-major, 64 x 64 x 64 tiles whose stages are
+// all inside M x N): each stage goes from global memory straight into LDS
+// (global_load_lds_dwordx4, no registers and no LDS store instructions), A
+// as rows of 64 k with k-quad q of tile row r in 16-byte slot (q + r) & 15
+// (a 16-lane read of 16 rows' quad q touches 16 distinct bank groups), B as
+// blocks of 4 k rows x 64 columns, the 16-byte column chunks of odd blocks
+// rotated by 8 (the half-waves read blocks q and q + 1: opposite halves of
+// the 64 banks); the operand reads and the MFMA sequence are those of
+// LOAD_VEC, so the results are bit-identical.
 enum {
     LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3, LOAD_NHWC_POOL = 4,
-    LOAD_PLANES = 5, LOAD_PLANES_POOL = 6, LOAD_TVEC = 7, LOAD_TSCALAR = 8
+    LOAD_PLANES = 5, LOAD_PLANES_POOL = 6, LOAD_TVEC = 7, LOAD_TSCALAR = 8, LOAD_DMA = 9
 };
 template <int M> constexpr bool is_trans = (M == LOAD_TVEC || M == LOAD_TSCALAR);
 
@@ -94,6 +103,12 @@ struct Tile {
     static constexpr int A_STAGE = KQ * A_PLANE;
     static constexpr int B_STAGE = KQ * B_PLANE;
     static constexpr int STAGE = A_STAGE + B_STAGE;
+    // LOAD_DMA stage: A as BM rows of BK floats, B as KQ blocks of 4 k rows
+    // x BN floats, unpadded, so that the two stage buffers are the first
+    // 64 KiB of LDS.
+    static constexpr int DA_STAGE = BM * BK;
+    static constexpr int DB_BLOCK = 4 * BN;
+    static constexpr int D_STAGE = DA_STAGE + KQ * DB_BLOCK;
     // 16-byte load items per stage; a thread takes items tid + i * THREADS.
     static constexpr int A_TOTAL = BM * KQ;
     static constexpr int B_TOTAL = KQ * (BN / 4);
@@ -152,7 +167,8 @@ struct GemmArgs {
 // Tiles whose epilogue can run the classifier head (GemmArgs::head_w).
 template <class T, int AMODE, int BMODE>
 constexpr bool head_tile = T::BM == 64 && T::BN == 64 && T::WK == 2 && T::FM == 1 && T::FN == 1 &&
-                           AMODE == LOAD_VEC && BMODE == LOAD_VEC;
+                           ((AMODE == LOAD_VEC && BMODE == LOAD_VEC) ||
+                            (AMODE == LOAD_DMA && BMODE == LOAD_DMA));
 constexpr int HEAD_MAX_N2 = 16;
 
 // (pixel, k-quad) of B item q of a stage: NHWC-style loaders put a pixel's
@@ -230,9 +246,42 @@ __device__ __forceinline__ void block_pos(int &local, int &split) {
     local = bid - split * nt;
 }
 
+// Tiles the LOAD_DMA stage loop serves: 64 rows of 16 k-quads (one 16-lane
+// row of a DMA instruction), B blocks of 64 columns, whole DMA instructions
+// per wave, and the EARLY stage schedule.
+template <class T>
+constexpr bool dma_tile = T::BK == 64 && T::BN == 64 && T::EARLY &&
+                          (T::BM / 4) % (T::THREADS / 64) == 0 && T::KQ % (T::THREADS / 64) == 0;
+
+// One 16-byte-per-lane LDS DMA (global_load_lds_dwordx4): lane l's 16
+// bytes at src land at LDS address dst + 16 l, dst (in M0) wave-uniform.
+// Inline assembly rather than the builtin: the compiler makes every LDS
+// read after the builtin wait for it (vmcnt(0)), which would expose the
+// whole DMA latency at the next operand read; here the loop's own
+// vmcnt(0) before the stage barrier is the only wait (so nothing may read
+// a stage's LDS before that barrier).  s_nop: the wait state an M0 write
+// needs before an LDS DMA.
+__device__ __forceinline__ uint32_t lds_address(const float *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
+}
+__device__ __forceinline__ void dma16(const float *src, const float *dst) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_address(dst)))
+                 : "memory");
+}
+// Waits for this wave's outstanding vector memory loads, LDS DMAs included.
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 template <class T, int AMODE, int BMODE>
 __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) float smem[2 * T::STAGE];
+    constexpr bool DMA = AMODE == LOAD_DMA;
+    static_assert(DMA == (BMODE == LOAD_DMA), "LOAD_DMA loads both operands");
+    static_assert(!DMA || dma_tile<T>, "LOAD_DMA tile shape");
+    static_assert(!DMA || 2 * T::D_STAGE * sizeof(float) <= 65536,
+                  "LDS DMA destinations within the first 64 KiB");
+    __shared__ __attribute__((aligned(16)))
+    float smem[2 * (DMA && T::D_STAGE > T::STAGE ? T::D_STAGE : T::STAGE)];
 
     const int tid = threadIdx.x;
     const int tiles_m = (g.M + T::BM - 1) / T::BM;
@@ -791,15 +840,140 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 4 * T::FM * T::FN, 0);
         }
     };
+    // ---- LOAD_DMA stage loop.  Per stage, wave w issues the DMAs of A row
+    // quads (4 rows x 64 k: lane l takes row 4i + l / 16 and fills its slot
+    // l % 16 with k-quad (l % 16 - row) & 15) and of B blocks b (4 k rows x
+    // 64 columns: lane l takes row l / 16 and fills its slot l % 16 with
+    // column chunk (l % 16 - 8 (b & 1)) & 15).  A stage
+    // is in flight from the barrier of stage kt - 2 (before that stage's last
+    // group, its buffer no longer read) to the barrier of stage kt - 1, whose
+    // vmcnt(0) waits for it; the loop has no register staging and no LDS
+    // stores.  A ragged first stage (k below 0) is loaded by the same lanes
+    // with guarded 16-byte loads and stores to the same LDS places.
+    auto dma_loop = [&](auto) {
+        if (nk <= 0) return;
+        constexpr int NW = T::THREADS / 64;
+        constexpr int DAI = T::BM / 4 / NW, DBI = T::KQ / NW; // DMAs per wave and stage
+        const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int du = lane >> 4, dc = lane & 15;
+        size_t a_src[DAI], b_src[DBI]; // element offsets at k = 0
+        int a_q[DAI];                  // the k-quad lane l fetches
+#pragma unroll
+        for (int j = 0; j < DAI; ++j) {
+            const int r = 4 * (wv * DAI + j) + du;
+            a_q[j] = (dc - r) & 15;
+            a_src[j] = (size_t)(m0 + r) * g.lda + 4 * a_q[j];
+        }
+#pragma unroll
+        for (int j = 0; j < DBI; ++j) {
+            const int blk = wv * DBI + j;
+            b_src[j] = (size_t)(4 * blk + du) * g.ldb + n0 + 4 * ((dc - 8 * (blk & 1)) & 15);
+        }
+        auto dma_stage = [&](int k0, int buf) {
+            float *As = smem + buf * T::D_STAGE, *Bs = As + T::DA_STAGE;
+#pragma unroll
+            for (int j = 0; j < DAI; ++j)
+                dma16(g.A + (a_src[j] + k0), As + (wv * DAI + j) * 4 * T::BK);
+#pragma unroll
+            for (int j = 0; j < DBI; ++j)
+                dma16(g.B + (b_src[j] + (size_t)k0 * g.ldb), Bs + (wv * DBI + j) * T::DB_BLOCK);
+        };
+        auto guarded_stage = [&](int k0) { // buffer 0
+            float *As = smem, *Bs = smem + T::DA_STAGE;
+#pragma unroll
+            for (int j = 0; j < DAI; ++j) {
+                const int k = k0 + 4 * a_q[j];
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k >= 0 && k < kend)
+                    v = *reinterpret_cast<const float4 *>(g.A + (a_src[j] + (ptrdiff_t)k0));
+                *reinterpret_cast<float4 *>(As + (wv * DAI + j) * 4 * T::BK + 4 * lane) = v;
+            }
+#pragma unroll
+            for (int j = 0; j < DBI; ++j) {
+                const int k = k0 + 4 * (wv * DBI + j) + du;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (k >= 0 && k < kend)
+                    v = *reinterpret_cast<const float4 *>(g.B + (b_src[j] + (ptrdiff_t)k0 * g.ldb));
+                *reinterpret_cast<float4 *>(Bs + (wv * DBI + j) * T::DB_BLOCK + 4 * lane) = v;
+            }
+        };
+        // operand reads: group s8 of k-group wk, half-wave h takes k-quad
+        // q = 2 GROUPS wk + 2 s8 + h (LOAD_VEC's order)
+        int a_rd[GROUPS][T::FM];
+#pragma unroll
+        for (int s8 = 0; s8 < GROUPS; ++s8)
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i) {
+                const int r = wm * T::WTM + i * 32 + r32, q = 2 * GROUPS * wk + 2 * s8 + half;
+                a_rd[s8][i] = r * T::BK + ((q + r) & 15) * 4;
+            }
+        int b_rd[T::FN]; // block parity = half
+#pragma unroll
+        for (int j = 0; j < T::FN; ++j) {
+            const int n = wn * T::WTN + j * 32 + r32;
+            b_rd[j] = (2 * GROUPS * wk + half) * T::DB_BLOCK + (((n >> 2) + 8 * half) & 15) * 4 +
+                      (n & 3);
+        }
+        auto fetch_dma = [&](int buf, int s8, float4 *fa, float4 *fb) {
+            const float *As = smem + buf * T::D_STAGE, *Bs = As + T::DA_STAGE;
+#pragma unroll
+            for (int i = 0; i < T::FM; ++i)
+                fa[i] = *reinterpret_cast<const float4 *>(As + a_rd[s8][i]);
+#pragma unroll
+            for (int j = 0; j < T::FN; ++j) {
+                const float *b = Bs + b_rd[j] + 2 * s8 * T::DB_BLOCK;
+                fb[j] = make_float4(b[0], b[T::BN], b[2 * T::BN], b[3 * T::BN]);
+            }
+        };
+        // LDS read instructions per group: A's 16-byte reads, B's 4 rows as
+        // two ds_read2st64_b32
+        constexpr int NMF = 4 * T::FM * T::FN, NRD = T::FM + 2 * T::FN;
+        static_assert(NMF >= NRD, "one MFMA before each operand read");
+        if (kbeg < 0)
+            guarded_stage(kbeg);
+        else
+            dma_stage(kbeg, 0);
+        if (nk > 1) dma_stage(kbeg + T::BK, 1);
+        wait_vm();
+        __syncthreads();
+        float4 fa[2][T::FM], fb[2][T::FN];
+        fetch_dma(0, 0, fa[0], fb[0]);
+        for (int kt = 0; kt < nk; ++kt) {
+            const int buf = kt & 1;
+#pragma unroll
+            for (int s8 = 0; s8 + 1 < GROUPS; ++s8) {
+                const int cur = s8 & 1;
+                fetch_dma(buf, s8 + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                mfma_group(fa[cur], fb[cur]);
+#pragma unroll
+                for (int r = 0; r < NRD; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
+            }
+            // waits for this wave's DMAs of stage kt + 1 (vmcnt) and its
+            // reads of stage kt (lgkmcnt), then the barrier
+            wait_vm();
+            __syncthreads();
+            if (kt + 2 < nk) dma_stage(kbeg + (kt + 2) * T::BK, buf);
+            if (kt + 1 < nk) fetch_dma(buf ^ 1, 0, fa[0], fb[0]);
+            mfma_group(fa[1], fb[1]);
+        }
+    };
     // The branch-free loop reads its last stage again past the end, unguarded
     // in a full tile, so that stage must be whole: a split whose only stage
     // is the ragged first one (K < BK) runs the guarded loop.
-    const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N) &&
-                           !(nk == 1 && kbeg < 0);
-    if (full_tile)
-        main_loop(std::true_type{});
-    else
-        main_loop(std::false_type{});
+    if constexpr (DMA) {
+        dma_loop(0);
+    } else {
+        const bool full_tile = m0 + T::BM <= g.M && (is_conv<BMODE> || n0 + T::BN <= g.N) &&
+                               !(nk == 1 && kbeg < 0);
+        if (full_tile)
+            main_loop(std::true_type{});
+        else
+            main_loop(std::false_type{});
+    }
 
     if constexpr (T::WK > 1) {
         // k-groups 1..WK-1 hand their sums to group 0 through LDS (free after
@@ -2283,16 +2457,35 @@ template <class T, int AMODE, int BMODE> int run_gemm(GemmArgs g, int splits, co
         using TB = BandTile<T>;
         const int band_tiles =
             (int)((int64_t)((g.M + TB::BM - 1) / TB::BM) * ((g.N - band.n_begin + TB::BN - 1) / TB::BN));
-        return launch_range<TB, AMODE, BMODE>(band, 0, band_tiles, 1, name);
+        // the band's small tiles take the register loaders (LOAD_DMA is for
+        // 64-column tiles)
+        constexpr int BA = AMODE == LOAD_DMA ? LOAD_VEC : AMODE;
+        constexpr int BB = BMODE == LOAD_DMA ? LOAD_VEC : BMODE;
+        return launch_range<TB, BA, BB>(band, 0, band_tiles, 1, name);
     }
     if (s.tail) return launch_range<T, AMODE, BMODE>(g, s.head, s.tail, s.tail_splits, name);
     return CAMEL_HIP_OK;
+}
+
+// True when the LOAD_DMA stage loop can run g: a tile shape it serves,
+// row-major operands with 16-byte rows (avec, bvec, 16-byte aligned leading
+// dimensions) and every tile inside M x N (the DMAs have no guards; only a
+// ragged first K stage is loaded with them).
+template <class T> bool dma_eligible(const GemmArgs &g, bool avec, bool bvec) {
+    if constexpr (dma_tile<T>)
+        return avec && bvec && g.M % T::BM == 0 && (g.N - g.n_begin) % T::BN == 0 &&
+               g.lda % 4 == 0 && g.ldb % 4 == 0;
+    return false;
 }
 
 // Runs the tile GEMM with the loaders the operands allow: A row-major or
 // (atrans) given transposed, each with 16-byte loads where avec / bvec.
 template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool bvec,
                                          bool atrans = false) {
+    if constexpr (dma_tile<T>) {
+        if (!atrans && dma_eligible<T>(g, avec, bvec))
+            return run_gemm<T, LOAD_DMA, LOAD_DMA>(g, splits, "sgemm_kernel");
+    }
     if (atrans) {
         if (avec && bvec) return run_gemm<T, LOAD_TVEC, LOAD_VEC>(g, splits, "sgemm_kernel");
         if (avec) return run_gemm<T, LOAD_TVEC, LOAD_SCALAR>(g, splits, "sgemm_kernel");
@@ -2309,7 +2502,11 @@ template <class T> int launch_gemm_modes(GemmArgs g, int splits, bool avec, bool
 template <class T> size_t gemm_modes_partial_bytes(const GemmArgs &g, int splits, bool avec,
                                                    bool bvec, bool atrans = false) {
     GemmSchedule s;
-    if (atrans) {
+    bool dma = false;
+    if constexpr (dma_tile<T>) dma = !atrans && dma_eligible<T>(g, avec, bvec);
+    if (dma) {
+        if constexpr (dma_tile<T>) s = schedule_gemm<T, LOAD_DMA, LOAD_DMA>(g, splits);
+    } else if (atrans) {
         if (avec && bvec)
             s = schedule_gemm<T, LOAD_TVEC, LOAD_VEC>(g, splits);
         else if (avec)
@@ -2338,7 +2535,12 @@ int launch_split_partials(GemmArgs g, int splits, bool avec, bool bvec, SplitPar
     const int tiles = tiles_m * tiles_n;
     int used = 0;
     float *at = nullptr;
-    if (avec && bvec)
+    bool dma = false;
+    if constexpr (dma_tile<T>) dma = dma_eligible<T>(g, avec, bvec);
+    if (dma) {
+        if constexpr (dma_tile<T>)
+            CAMEL_RETURN_IF((launch_range<T, LOAD_DMA, LOAD_DMA>(g, 0, tiles, splits, "sgemm_kernel", &used, &at)));
+    } else if (avec && bvec)
         CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_VEC>(g, 0, tiles, splits, "sgemm_kernel", &used, &at)));
     else if (avec)
         CAMEL_RETURN_IF((launch_range<T, LOAD_VEC, LOAD_SCALAR>(g, 0, tiles, splits, "sgemm_kernel", &used, &at)));
@@ -3214,8 +3416,12 @@ int camel_hip_dense_head(const float *x, const float *w1, const float *b1, const
         g.head_w = w2;
         g.head_partial = part.f();
         g.head_n2 = (int)N2;
-        CAMEL_RETURN_IF((launch_range<TileSmall, LOAD_VEC, LOAD_VEC>(g, 0, tiles_m * tiles_n, 1,
-                                                                      "sgemm_kernel")));
+        if (dma_eligible<TileSmall>(g, avec, bvec))
+            CAMEL_RETURN_IF((launch_range<TileSmall, LOAD_DMA, LOAD_DMA>(g, 0, tiles_m * tiles_n, 1,
+                                                                          "sgemm_kernel")));
+        else
+            CAMEL_RETURN_IF((launch_range<TileSmall, LOAD_VEC, LOAD_VEC>(g, 0, tiles_m * tiles_n, 1,
+                                                                          "sgemm_kernel")));
         const unsigned blocks = (unsigned)((M + 3) / 4);
         if (softmax)
             hipLaunchKernelGGL(head_finish_kernel<true>, dim3(blocks), dim3(256), 0, stream(), part.f(),
