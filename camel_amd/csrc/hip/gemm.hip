@@ -2641,9 +2641,12 @@ constexpr int CP_IR = CP_R1 + 2;          // input rows a band reads (12)
 // their chunks are distinct mod 16 (64 banks x 4 bytes); those 16 lanes read
 // a 2 x 2 block of windows, pixels (2 py + r, 2 px + c) for r, c in 0..3, and
 // with a row pitch of CP_RS = 28 pixels (28 r = 0, 12, 8, 4 mod 16) the 16
-// chunks are distinct.  (4 windows of one row, 2 rows x 8 pixels, collided
-// 2-way on 4 of the chunks at this pitch; a pitch of 40 clears those too but
-// ran the CNN forward 1.7% slower; the 2 x 2 blocks ran it 0.4% faster.)
+// chunks are distinct.  (4 windows of one row, 2 rows x 8 pixels, put 4
+// chunks on 2 lanes each at this pitch; a pitch of 40 separates those too but
+// ran the CNN forward 1.7% slower; the 2 x 2 blocks ran it 0.4% faster.  The
+// kernel's SQ_LDS_BANK_CONFLICT share reads 28.5% with either mapping at this
+// pitch and 0 at pitch 40, so what that counter counts here is not explained
+// by this model of the patch reads.)
 constexpr int CP_RS = 28;
 static_assert(CP_RS >= CP_OW1 && CP_RS % 16 == 12, "conflict-free patch row pitch");
 // One channel quad of the patch: 1120 floats, padded to 1124 (= 4 mod 32) so
