@@ -57,15 +57,15 @@ constexpr int GROUP_M = 4;
 // At [K, M] row-major (A[m][k] = At[k][m]): like B, k rows with the tile's
 // m contiguous, transposed 4x4 in registers before the LDS store, so
 // transpose(X) @ E needs no copy of X (16-byte loads need M % 4 == 0).
-// LOAD_DMA (A and B together, row-major, 64 x 64 x 64 tiles whose stages are
-// all inside M x N): each stage goes from global memory straight into LDS
+// LOAD_DMA (A and B together, row-major, BK = 64 tiles whose stages are all
+// inside M x N): each stage goes from global memory straight into LDS
 // (global_load_lds_dwordx4, no registers and no LDS store instructions), A
 // as rows of 64 k with k-quad q of tile row r in 16-byte slot (q + r) & 15
 // (a 16-lane read of 16 rows' quad q touches 16 distinct bank groups), B as
-// blocks of 4 k rows x 64 columns, the 16-byte column chunks of odd blocks
-// rotated by 8 (the half-waves read blocks q and q + 1: opposite halves of
-// the 64 banks); the operand reads and the MFMA sequence are those of
-// LOAD_VEC, so the results are bit-identical.
+// blocks of 4 k rows x BN columns stored as 64-column pieces, the 16-byte
+// column chunks of odd blocks rotated by 8 (the half-waves read blocks q and
+// q + 1: opposite halves of the 64 banks); the operand reads and the MFMA
+// sequence are those of LOAD_VEC, so the results are bit-identical.
 enum {
     LOAD_VEC = 0, LOAD_SCALAR = 1, LOAD_CONV = 2, LOAD_NHWC = 3, LOAD_NHWC_POOL = 4,
     LOAD_PLANES = 5, LOAD_PLANES_POOL = 6, LOAD_TVEC = 7, LOAD_TSCALAR = 8, LOAD_DMA = 9
@@ -104,8 +104,8 @@ struct Tile {
     static constexpr int B_STAGE = KQ * B_PLANE;
     static constexpr int STAGE = A_STAGE + B_STAGE;
     // LOAD_DMA stage: A as BM rows of BK floats, B as KQ blocks of 4 k rows
-    // x BN floats, unpadded, so that the two stage buffers are the first
-    // 64 KiB of LDS.
+    // x BN floats, each block BN / 64 DMA pieces of 4 rows x 64 floats,
+    // unpadded.
     static constexpr int DA_STAGE = BM * BK;
     static constexpr int DB_BLOCK = 4 * BN;
     static constexpr int D_STAGE = DA_STAGE + KQ * DB_BLOCK;
@@ -246,12 +246,15 @@ __device__ __forceinline__ void block_pos(int &local, int &split) {
     local = bid - split * nt;
 }
 
-// Tiles the LOAD_DMA stage loop serves: 64 rows of 16 k-quads (one 16-lane
-// row of a DMA instruction), B blocks of 64 columns, whole DMA instructions
-// per wave, and the EARLY stage schedule.
+// Tiles the LOAD_DMA stage loop serves (it has its own stage schedule):
+// rows of 16 k-quads (one 16-lane row of a DMA instruction), B blocks of
+// whole 64-column pieces, whole DMA instructions per wave.  Measured on the
+// 64 x 64 tile (MLP, 1024^3, CNN dense1) and the one-round 128 x 128 tile
+// with k-groups (2048^3).
 template <class T>
-constexpr bool dma_tile = T::BK == 64 && T::BN == 64 && T::EARLY &&
-                          (T::BM / 4) % (T::THREADS / 64) == 0 && T::KQ % (T::THREADS / 64) == 0;
+constexpr bool dma_tile = T::BK == 64 && T::BN % 64 == 0 && T::BM % 64 == 0 && T::WK == 2 &&
+                          (T::BM / 4) % (T::THREADS / 64) == 0 &&
+                          (T::KQ * T::BN / 64) % (T::THREADS / 64) == 0;
 
 // One 16-byte-per-lane LDS DMA (global_load_lds_dwordx4): lane l's 16
 // bytes at src land at LDS address dst + 16 l, dst (in M0) wave-uniform.
@@ -278,8 +281,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     constexpr bool DMA = AMODE == LOAD_DMA;
     static_assert(DMA == (BMODE == LOAD_DMA), "LOAD_DMA loads both operands");
     static_assert(!DMA || dma_tile<T>, "LOAD_DMA tile shape");
-    static_assert(!DMA || 2 * T::D_STAGE * sizeof(float) <= 65536,
-                  "LDS DMA destinations within the first 64 KiB");
+    static_assert(!DMA || 2 * T::D_STAGE * sizeof(float) <= 160 * 1024, "two DMA stages in LDS");
     __shared__ __attribute__((aligned(16)))
     float smem[2 * (DMA && T::D_STAGE > T::STAGE ? T::D_STAGE : T::STAGE)];
 
@@ -853,7 +855,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
     auto dma_loop = [&](auto) {
         if (nk <= 0) return;
         constexpr int NW = T::THREADS / 64;
-        constexpr int DAI = T::BM / 4 / NW, DBI = T::KQ / NW; // DMAs per wave and stage
+        constexpr int BP = T::BN / 64;                             // 64-column pieces per B block
+        // DMAs per wave and stage (at least 1: this body is compiled for every tile)
+        constexpr int DAI = T::BM / 4 / NW > 0 ? T::BM / 4 / NW : 1;
+        constexpr int DBI = T::KQ * BP / NW > 0 ? T::KQ * BP / NW : 1;
         const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int du = lane >> 4, dc = lane & 15;
         size_t a_src[DAI], b_src[DBI]; // element offsets at k = 0
@@ -866,8 +871,8 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         }
 #pragma unroll
         for (int j = 0; j < DBI; ++j) {
-            const int blk = wv * DBI + j;
-            b_src[j] = (size_t)(4 * blk + du) * g.ldb + n0 + 4 * ((dc - 8 * (blk & 1)) & 15);
+            const int pc = wv * DBI + j, blk = pc / BP, h = pc - blk * BP;
+            b_src[j] = (size_t)(4 * blk + du) * g.ldb + n0 + 64 * h + 4 * ((dc - 8 * (blk & 1)) & 15);
         }
         auto dma_stage = [&](int k0, int buf) {
             float *As = smem + buf * T::D_STAGE, *Bs = As + T::DA_STAGE;
@@ -876,7 +881,7 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 dma16(g.A + (a_src[j] + k0), As + (wv * DAI + j) * 4 * T::BK);
 #pragma unroll
             for (int j = 0; j < DBI; ++j)
-                dma16(g.B + (b_src[j] + (size_t)k0 * g.ldb), Bs + (wv * DBI + j) * T::DB_BLOCK);
+                dma16(g.B + (b_src[j] + (size_t)k0 * g.ldb), Bs + (wv * DBI + j) * 256);
         };
         auto guarded_stage = [&](int k0) { // buffer 0
             float *As = smem, *Bs = smem + T::DA_STAGE;
@@ -890,11 +895,11 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
             }
 #pragma unroll
             for (int j = 0; j < DBI; ++j) {
-                const int k = k0 + 4 * (wv * DBI + j) + du;
+                const int k = k0 + 4 * ((wv * DBI + j) / BP) + du;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (k >= 0 && k < kend)
                     v = *reinterpret_cast<const float4 *>(g.B + (b_src[j] + (ptrdiff_t)k0 * g.ldb));
-                *reinterpret_cast<float4 *>(Bs + (wv * DBI + j) * T::DB_BLOCK + 4 * lane) = v;
+                *reinterpret_cast<float4 *>(Bs + (wv * DBI + j) * 256 + 4 * lane) = v;
             }
         };
         // operand reads: group s8 of k-group wk, half-wave h takes k-quad
@@ -910,9 +915,9 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
         int b_rd[T::FN]; // block parity = half
 #pragma unroll
         for (int j = 0; j < T::FN; ++j) {
-            const int n = wn * T::WTN + j * 32 + r32;
-            b_rd[j] = (2 * GROUPS * wk + half) * T::DB_BLOCK + (((n >> 2) + 8 * half) & 15) * 4 +
-                      (n & 3);
+            const int n = wn * T::WTN + j * 32 + r32, c = n & 63;
+            b_rd[j] = (2 * GROUPS * wk + half) * T::DB_BLOCK + (n >> 6) * 256 +
+                      (((c >> 2) + 8 * half) & 15) * 4 + (c & 3);
         }
         auto fetch_dma = [&](int buf, int s8, float4 *fa, float4 *fb) {
             const float *As = smem + buf * T::D_STAGE, *Bs = As + T::DA_STAGE;
@@ -922,12 +927,13 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int j = 0; j < T::FN; ++j) {
                 const float *b = Bs + b_rd[j] + 2 * s8 * T::DB_BLOCK;
-                fb[j] = make_float4(b[0], b[T::BN], b[2 * T::BN], b[3 * T::BN]);
+                fb[j] = make_float4(b[0], b[64], b[128], b[192]);
             }
         };
         // LDS read instructions per group: A's 16-byte reads, B's 4 rows as
         // two ds_read2st64_b32
         constexpr int NMF = 4 * T::FM * T::FN, NRD = T::FM + 2 * T::FN;
+        constexpr int SPACE = NMF >= 2 * NRD ? 2 : 1; // MFMAs before each operand read
         static_assert(NMF >= NRD, "one MFMA before each operand read");
         if (kbeg < 0)
             guarded_stage(kbeg);
@@ -947,10 +953,10 @@ __global__ __launch_bounds__(T::THREADS) void sgemm_kernel(GemmArgs g) {
                 mfma_group(fa[cur], fb[cur]);
 #pragma unroll
                 for (int r = 0; r < NRD; ++r) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, SPACE, 0);
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, NMF - SPACE * NRD, 0);
             }
             // waits for this wave's DMAs of stage kt + 1 (vmcnt) and its
             // reads of stage kt (lgkmcnt), then the barrier
