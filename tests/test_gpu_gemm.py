@@ -42,10 +42,36 @@ def test_sgemm_matches_oracle(M, N, Kd):
 
 
 @pytest.mark.parametrize("M,N,Kd", [
+    (1024, 1024, 784),   # 64x64 tiles (the MLP's first layer), ragged first stage
+    (512, 128, 9216),    # 64x64 tiles with 16 K splits (the CNN's dense1)
+    (1024, 1024, 1024),  # 64x64 tiles, whole stages
+    (2048, 2048, 1000),  # one-round 128x128 tiles with k-groups, ragged first stage
+])
+def test_lds_dma_path_equals_register_path(M, N, Kd):
+    # Row-major operands with 16-byte rows and M, N multiples of the tile take
+    # the LDS DMA stage loop (global_load_lds straight into LDS); one row less
+    # (M - 1, the same tile grid and K splits) takes the register-staged
+    # loaders of the same tile.  Both feed the MFMAs the same values in the
+    # same order, so the rows they share are bit-identical on random floats
+    # (bias and relu too).
+    a, b = _ab(M, N, Kd, 0x1700 + M + N + Kd)
+    bias = D.uniform(0x1701 + N, (N,), -1.0, 1.0)
+    flags = H.EPI_BIAS | H.EPI_RELU
+    dma = K.sgemm(a, b, bias, flags)
+    staged = K.sgemm(a[:M - 1], b, bias, flags)
+    assert np.array_equal(dma[:M - 1].view(np.uint32), staged.view(np.uint32))
+    # and the DMA path's first rows against the oracle (no bias or relu)
+    plain = K.sgemm(a, b)[:64]
+    ok, worst = K.gemm_tol_ok(plain, O.matmul(a[:64], b), a[:64], b)
+    assert ok, f"worst error / bound = {worst}"
+
+
+@pytest.mark.parametrize("M,N,Kd", [
     (512, 256, 2000),    # 64x64 tiles, 7 K splits, K % 64 = 16
     (1024, 2048, 1000),  # 64x64 tiles, no split, K % 64 = 40
     (2048, 2048, 1001),  # 128x128 tiles, odd K (scalar A loads), K % 32 = 9
     (2000, 2100, 1000),  # 128x128 tiles in two k-groups (one round), K % 64 = 40
+    (2048, 2048, 1000),  # the same tiles staged by LDS DMA (M, N multiples of 128)
     (4096, 4096, 1000),  # 256x256 tiles, K % 32 = 8
     (200, 72, 1000),     # 32x32 tiles, K splits, K % 64 = 40
 ])
