@@ -46,6 +46,8 @@ struct State {
 constexpr int STAGING_SLOTS = 3;
 constexpr size_t STAGING_SLOT_BYTES = size_t(8) << 20;
 constexpr size_t STAGING_MIN_BYTES = size_t(2) << 20;
+static_assert(sizeof(State::slot_done) / sizeof(hipEvent_t) == STAGING_SLOTS,
+              "one completion event per staging slot");
 
 State &state() {
     static State s;
